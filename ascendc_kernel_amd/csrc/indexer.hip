@@ -1,0 +1,567 @@
+// Task2: lightning indexer (RoPE + relu-weighted multi-head score + causal
+// mask + top-k) on gfx950 (MI355X).
+//
+// Semantics follow Model.forward of reference/task2_v0_ref.py:123-144 after the
+// two projections, reproducing the rounding torch applies on the same GPU:
+//   RoPE   (:93-104,131)  q[..., d-rd:] *= freqs_cis as complex, rounded to bf16
+//   w      (:132)         bf16(fp32(wl) * w_scale)
+//   S      (:133)         bf16(q . k), fp32 accumulate in channel order 0..d-1
+//   score  (:134)         bf16(sum_h bf16(relu(S_h) * w_h)); the fp32 head sum uses
+//                         four accumulators (heads j, j+4, j+8, j+12 for j = 0..3)
+//                         combined as ((a0 + a1) + a2) + a3
+//   mask   (:135-137)     k >= (t+1)//ratio -> -inf
+//   top-k  (:138)         value descending, ties by index ascending
+//   fill   (:139-143)     masked picks -> -1, others + offset
+// The rounding rules were established on the MI355X against torch 2.10-ROCm
+// with planted inputs (GEMM: MFMA in channel order; head sum: the accumulator
+// pattern above; RoPE: see rope_pair).
+//
+// One wave owns two consecutive tokens of one batch. Their 2 x 16 head rows
+// form the A operand of v_mfma_f32_32x32x16_bf16 against 32 candidate keys per
+// tile; v_permlane32_swap then gives every lane all 16 head scores of one
+// (token, candidate), so the epilogue and the head sum are lane-local. Scores
+// become 16-bit order keys in LDS; a two-pass 8-bit radix select per half-wave
+// finds the k-th key, ties are taken in index order with ballots, and the k
+// winners are bitonic-sorted on a (key, ~index) composite before the int64
+// indices are written. Waves take token pairs from the end of the sequence
+// first, so the longest causal rows start first.
+#include "dsa_common.h"
+
+using namespace dsa;
+
+namespace {
+
+constexpr int kH = 16;  // index heads handled by the fused kernel
+constexpr int kD = 64;  // index head dim handled by the fused kernel
+
+// One complex product of RoPE in the rounding torch uses.
+//  DSA_ROPE_CPU: vectorised CPU kernel, every product rounded, no FMA.
+//  DSA_ROPE_TORCH_ROCM: the broadcast elementwise kernel of torch-ROCm; its
+//  unrolled loop contracts unroll slots 0..2 as re = fma(a, c, -(b*d)),
+//  im = fma(b, c, a*d) and slot 3 as re = fma(-b, d, a*c), im = (a*d) + (b*c),
+//  where slot = (n / 128) % 4 for the flat index n of the complex element in the
+//  [b, s, h, rd/2] tensor (measured: 1.33 M of 1.33 M elements agree bit for bit).
+__device__ __forceinline__ void rope_pair(float a, float b, float c, float d, int mode,
+                                          int64_t n, float& re, float& im) {
+  if (mode == DSA_ROPE_CPU) {
+    re = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, d));
+    im = __fadd_rn(__fmul_rn(a, d), __fmul_rn(b, c));
+  } else if (((n >> 7) & 3) != 3) {
+    re = __fmaf_rn(a, c, -__fmul_rn(b, d));
+    im = __fmaf_rn(b, c, __fmul_rn(a, d));
+  } else {
+    re = __fmaf_rn(-b, d, __fmul_rn(a, c));
+    im = __fadd_rn(__fmul_rn(a, d), __fmul_rn(b, c));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Standalone in-place RoPE: one thread per complex pair.
+struct RopeParams {
+  uint16_t* q;
+  const float* freqs;  // [s, rd/2, 2]
+  int64_t rows;        // b * s * h
+  int32_t S, H, D, rd, mode;
+};
+
+__global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
+  const int half_rd = p.rd >> 1;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.rows * half_rd) return;
+  const int64_t row = gid / half_rd;
+  const int j = (int)(gid - row * half_rd);
+  const int t = (int)((row / p.H) % p.S);
+  uint32_t* w = reinterpret_cast<uint32_t*>(p.q + row * p.D + (p.D - p.rd) + 2 * j);
+  const uint32_t x = *w;
+  const float c = p.freqs[((int64_t)t * half_rd + j) * 2];
+  const float d = p.freqs[((int64_t)t * half_rd + j) * 2 + 1];
+  float re, im;
+  rope_pair(bf_lo(x), bf_hi(x), c, d, p.mode, gid, re, im);
+  *w = pack_bf2(re, im);
+}
+
+// ---------------------------------------------------------------------------
+// Fused score + top-k.
+struct IxParams {
+  const uint16_t* q;    // [B, S, 16, 64]
+  const uint16_t* kv;   // row k of batch b at kv + b*kvbs + k*64
+  int64_t kvbs;
+  const uint16_t* wl;   // [B, S, 16]
+  float wscale;
+  const float* freqs;   // [S, rd/2, 2] or nullptr
+  int32_t rope_mode;
+  int64_t* out;         // [B, S, K]
+  uint16_t* scores;     // optional [B, S, T] bf16 score dump (masked entries -inf)
+  int32_t B, S, rd, T, K, ratio, causal;
+  int64_t offset;
+  int32_t npairs;       // ceil(S / 2)
+  int32_t keys_bytes;   // LDS bytes of the key area of one wave (16-byte multiple)
+  int32_t wave_bytes;   // LDS bytes per wave
+};
+
+__device__ __forceinline__ int n_valid(const IxParams& p, int t) {
+  if (t >= p.S) return 0;
+  if (!p.causal) return p.T;
+  const int n = (t + 1) / p.ratio;
+  return n < p.T ? n : p.T;
+}
+
+__device__ __forceinline__ void lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
+// Per half-wave: the bin b of a 256-bin histogram (bins ascending in key) with
+// count(bins > b) < need <= count(bins >= b); returns -1 when the half holds
+// fewer than `need` entries. `gt` receives count(bins > b).
+__device__ __forceinline__ int find_bin(const uint32_t* hist, int lane, uint32_t need, uint32_t& gt) {
+  const int hl = lane & 31, half = lane >> 5;
+  const u32x4 lo4 = *reinterpret_cast<const u32x4*>(hist + 8 * hl);
+  const u32x4 hi4 = *reinterpret_cast<const u32x4*>(hist + 8 * hl + 4);
+  const uint32_t bins[8] = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+  uint32_t local = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) local += bins[i];
+  uint32_t incl = local;
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1) {
+    const uint32_t o = __shfl(incl, (lane + off) & 63, 64);
+    if (hl + off < 32) incl += o;
+  }
+  uint32_t cum = incl - local;
+  int fb = -1;
+  uint32_t fgt = 0;
+#pragma unroll
+  for (int i = 7; i >= 0; --i) {
+    const uint32_t nc = cum + bins[i];
+    if (cum < need && nc >= need) {
+      fb = 8 * hl + i;
+      fgt = cum;
+    }
+    cum = nc;
+  }
+  const uint32_t hm = (uint32_t)(__ballot(fb >= 0) >> (32 * half));
+  const int src = hm ? (int)(__builtin_ctz(hm)) + 32 * half : lane;
+  const int b = __shfl(fb, src, 64);
+  gt = __shfl(fgt, src, 64);
+  return hm ? b : -1;
+}
+
+template <int E>
+__global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int KP = 32 * E;  // sort size per half-wave
+  const int lane = threadIdx.x & 63;
+  const int wi = threadIdx.x >> 6;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + wi;
+  if (gw >= (int64_t)p.B * p.npairs) return;
+  const int pr = p.npairs - 1 - (int)(gw / p.B);  // longest rows first
+  const int b = (int)(gw % p.B);
+  const int t0 = 2 * pr;
+  const int half = lane >> 5, hl = lane & 31;
+  const int t = t0 + half;
+
+  unsigned char* wbase = smem + (size_t)wi * p.wave_bytes;
+  uint16_t* keys = reinterpret_cast<uint16_t*>(wbase) ;                // [2][NT][32]
+  uint32_t* hist = reinterpret_cast<uint32_t*>(wbase + p.keys_bytes);   // [2][256]
+  uint32_t* sbuf = hist + 512;                                         // [2][KP]
+  uint32_t* myhist = hist + 256 * half;
+  uint32_t* mysbuf = sbuf + KP * half;
+
+  const int nv = n_valid(p, t);
+  const int tlast = (t0 + 1 < p.S) ? t0 + 1 : t0;
+  const int nv_max = n_valid(p, tlast) > n_valid(p, t0) ? n_valid(p, tlast) : n_valid(p, t0);
+  const int ntile = (nv_max + 31) >> 5;
+  const int ntile_all = (p.keys_bytes / 128);
+
+  // Head weights of this half's token, bf16(fp32(wl) * w_scale), fp32 copies.
+  float w[kH];
+  if (t < p.S) {
+    const u32x4* wp = reinterpret_cast<const u32x4*>(p.wl + ((int64_t)b * p.S + t) * kH);
+    const u32x4 w0 = wp[0], w1 = wp[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[2 * i] = bf2f(f2bf(bf_lo(w0[i]) * p.wscale));
+      w[2 * i + 1] = bf2f(f2bf(bf_hi(w0[i]) * p.wscale));
+      w[8 + 2 * i] = bf2f(f2bf(bf_lo(w1[i]) * p.wscale));
+      w[8 + 2 * i + 1] = bf2f(f2bf(bf_hi(w1[i]) * p.wscale));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kH; ++i) w[i] = 0.f;
+  }
+
+  // A operand: row i = lane % 32 is (token t0 + i/16, head i%16); lane holds
+  // channels 16ks + 8(lane/32) .. +7 of that row, RoPE applied when asked.
+  bf16x8 qa[4];
+  {
+    const int tq = t0 + ((lane & 31) >> 4);
+    const int hq = lane & 15;
+    const int hsel = lane >> 5;
+    if (tq < p.S) {
+      const int64_t row = ((int64_t)b * p.S + tq) * kH + hq;
+      const uint16_t* src = p.q + row * kD;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * ks + 8 * hsel);
+        if (p.freqs != nullptr) {
+          const int half_rd = p.rd >> 1;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int dch = 16 * ks + 8 * hsel + 2 * jj;
+            const int pj = (dch - (kD - p.rd)) >> 1;
+            if (dch >= kD - p.rd) {
+              const float c = p.freqs[((int64_t)tq * half_rd + pj) * 2];
+              const float d = p.freqs[((int64_t)tq * half_rd + pj) * 2 + 1];
+              const int64_t n = row * half_rd + pj;
+              float re, im;
+              rope_pair(bf_lo(v[jj]), bf_hi(v[jj]), c, d, p.rope_mode, n, re, im);
+              v[jj] = pack_bf2(re, im);
+            }
+          }
+        }
+        qa[ks] = __builtin_bit_cast(bf16x8, v);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qa[ks] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+
+  // Zero this half's histogram (8 bins per lane).
+  *reinterpret_cast<u32x4*>(myhist + 8 * hl) = u32x4{0u, 0u, 0u, 0u};
+  *reinterpret_cast<u32x4*>(myhist + 8 * hl + 4) = u32x4{0u, 0u, 0u, 0u};
+  lds_fence();
+
+  const uint16_t* kvb = p.kv + (int64_t)b * p.kvbs;
+  const int kcol = lane & 31;
+  const int khalf = lane >> 5;
+  for (int tile = 0; tile < ntile; ++tile) {
+    // B operand: candidate 32*tile + lane%32, channels 16ks + 8(lane/32) .. +7.
+    const int cand = 32 * tile + kcol;
+    bf16x8 kb[4];
+    if (cand < p.T) {
+      const uint16_t* src = kvb + (int64_t)cand * kD + 8 * khalf;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        kb[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(src + 16 * ks));
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kb[ks] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    }
+    f32x16 acc = {};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = mfma32x32x16(qa[ks], kb[ks], acc);
+
+    // relu + the einsum's bf16 rounding, two heads per word: word k holds slots 2k, 2k+1.
+    uint32_t pk[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pk[k] = pack_bf2(fmaxf(acc[2 * k], 0.f), fmaxf(acc[2 * k + 1], 0.f));
+    // Exchange halves: afterwards lanes 0..31 hold token t0, lanes 32..63 token
+    // t0+1, all 16 heads of candidate 32*tile + lane%32. Slot r holds head
+    // r (r<4), r+4 (4<=r<8), r-4 (8<=r<12), r (12<=r). (The swap operands are
+    // computed words, never raw accumulator elements.)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(pk[k], pk[k + 4], false, false);
+      pk[k] = (uint32_t)sw[0];
+      pk[k + 4] = (uint32_t)sw[1];
+    }
+    // * w -> bf16, as fp32 values.
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int r = 2 * k;
+      const int h0 = (r < 4) ? r : (r < 8) ? r + 4 : (r < 12) ? r - 4 : r;
+      const uint32_t pb = pack_bf2(bf_lo(pk[k]) * w[h0], bf_hi(pk[k]) * w[h0 + 1]);
+      v[r] = bf_lo(pb);
+      v[r + 1] = bf_hi(pb);
+    }
+    // Head j is in slot j (j<4), j+4 -> slot j+8, j+8 -> slot j+4, j+12 -> slot j+12.
+    float a4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a4[j] = (((0.0f + v[j]) + v[j + 8]) + v[j + 4]) + v[j + 12];
+    const float tot = ((a4[0] + a4[1]) + a4[2]) + a4[3];
+    uint16_t sc = f2bf(tot);
+    const int c = 32 * tile + hl;
+    const bool valid = c < nv;
+    if (p.causal) sc = f2bf(bf2f(sc) + 0.0f);  // the reference adds the 0/-inf mask
+    uint16_t u = (uint16_t)(sc ^ ((sc & 0x8000u) ? 0xffffu : 0x8000u));
+    if ((sc & 0x7fffu) > 0x7f80u) u = 0xffffu;  // NaN ranks above everything
+    keys[(half * ntile_all + tile) * 32 + hl] = valid ? u : (uint16_t)0;
+    if (p.scores != nullptr && t < p.S && c < p.T)
+      p.scores[((int64_t)b * p.S + t) * p.T + c] = valid ? sc : (uint16_t)0xff80u;
+    if (valid) atomicAdd(&myhist[u >> 8], 1u);
+  }
+  if (p.out == nullptr) {  // score dump only: fill the never-valid tail with -inf
+    if (t < p.S)
+      for (int c = 32 * ntile + hl; c < p.T; c += 32)
+        p.scores[((int64_t)b * p.S + t) * p.T + c] = (uint16_t)0xff80u;
+    return;
+  }
+  lds_fence();
+
+  // The reference ranks all T candidates; masked ones carry -inf (order key
+  // 0x007f). Their count is known, so they enter the histograms analytically.
+  constexpr uint32_t kNegInfKey = 0x007fu;
+  const uint32_t K = (uint32_t)p.K;
+  const uint32_t nmask = (t < p.S) ? (uint32_t)(p.T - nv) : 0u;
+  if (hl == 0 && nmask > 0) atomicAdd(&myhist[kNegInfKey >> 8], nmask);
+  lds_fence();
+
+  // Radix select of the K-th largest key: two 8-bit passes.
+  uint32_t gt1 = 0, gt2 = 0;
+  const int b1 = find_bin(myhist, lane, K, gt1);
+  lds_fence();
+  *reinterpret_cast<u32x4*>(myhist + 8 * hl) = u32x4{0u, 0u, 0u, 0u};
+  *reinterpret_cast<u32x4*>(myhist + 8 * hl + 4) = u32x4{0u, 0u, 0u, 0u};
+  lds_fence();
+  for (int tile = 0; tile < ntile; ++tile) {
+    const int c = 32 * tile + hl;
+    const uint16_t u = keys[(half * ntile_all + tile) * 32 + hl];
+    if (c < nv && (int)(u >> 8) == b1) atomicAdd(&myhist[u & 255u], 1u);
+  }
+  if (hl == 0 && nmask > 0 && b1 == (int)(kNegInfKey >> 8)) atomicAdd(&myhist[kNegInfKey & 255u], nmask);
+  lds_fence();
+  const int b0 = find_bin(myhist, lane, K - gt1, gt2);
+  const bool real = (t < p.S) && b1 >= 0 && b0 >= 0;
+  const uint32_t V = real ? (((uint32_t)b1 << 8) | (uint32_t)b0) : 0x10000u;  // 0x10000: nothing matches
+  const uint32_t n_gt = real ? gt1 + gt2 : 0u;   // picks strictly above the k-th key
+  const uint32_t need_eq = real ? K - n_gt : 0u; // picks equal to it, lowest index first
+
+  // Gather the K picks in torch's order: [keys > V in index order] then
+  // [keys == V in index order], masked -inf candidates counting as index >= nv.
+  // E > 1: entry = (key << 16) | ~index, later sorted as a whole (stable order).
+  // E = 1: entry = (float-order key << 16) | valid << 15 | index, in gather order.
+  auto entry = [&](uint32_t u, uint32_t c) -> uint32_t {
+    if (E == 1) {
+      const uint32_t fk = (u == 0x7fffu) ? 0x8000u : u;  // -0 == +0 for the comparator
+      return (fk << 16) | 0x8000u | c;
+    }
+    return (u << 16) | (0xffffu - c);
+  };
+  const uint32_t ltmask = (1u << hl) - 1u;
+  uint32_t gt_run = 0, eq_run = 0;
+  for (int tile = 0; tile < ntile; ++tile) {
+    const int c = 32 * tile + hl;
+    const uint32_t u = keys[(half * ntile_all + tile) * 32 + hl];
+    const bool valid = c < nv;
+    const bool gt = valid && u > V;
+    const bool eq = valid && u == V;
+    const uint32_t gm = (uint32_t)(__ballot(gt) >> (32 * half));
+    const uint32_t em = (uint32_t)(__ballot(eq) >> (32 * half));
+    if (gt) {
+      const uint32_t pos = gt_run + __builtin_popcount(gm & ltmask);
+      if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
+    }
+    const uint32_t er = eq_run + __builtin_popcount(em & ltmask);
+    if (eq && er < need_eq) {
+      const uint32_t pos = n_gt + er;
+      if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
+    }
+    gt_run += __builtin_popcount(gm);
+    eq_run += __builtin_popcount(em);
+  }
+  const uint32_t eq_taken = eq_run < need_eq ? eq_run : need_eq;
+  if (V == kNegInfKey) {
+    // the remaining ties are masked candidates nv, nv+1, ...
+    for (uint32_t j = (uint32_t)hl; j < need_eq - eq_taken; j += 32) {
+      const uint32_t pos = n_gt + eq_taken + j;
+      if (pos < (uint32_t)KP) mysbuf[pos] = entry(kNegInfKey, (uint32_t)nv + j);
+    }
+  }
+  const uint32_t nsel = real ? K : 0u;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const uint32_t e = (uint32_t)(hl * E + i);
+    if (e >= nsel) mysbuf[e] = 0u;  // E > 1: sorts last; E = 1: invalid slot
+  }
+  lds_fence();
+
+  uint32_t sv[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) sv[i] = mysbuf[hl * E + i];
+
+  if (E > 1) {
+    // k > 32: torch sorts the gathered picks stably by value, i.e. value
+    // descending then index ascending = descending order of the entries.
+    // Bitonic sort (descending) of KP entries, E per lane, element e = hl*E + i.
+#pragma unroll
+    for (int k = 2; k <= KP; k <<= 1) {
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        if (j >= E) {
+          const int lj = j / E;
+#pragma unroll
+          for (int i = 0; i < E; ++i) {
+            const uint32_t o = (uint32_t)__shfl_xor((int)sv[i], lj, 64);
+            const int e = hl * E + i;
+            const bool lower = (e & j) == 0;
+            const bool desc = (e & k) == 0;
+            const bool keep_max = (lower == desc);
+            sv[i] = keep_max ? (sv[i] > o ? sv[i] : o) : (sv[i] < o ? sv[i] : o);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < E; ++i) {
+            if ((i & j) == 0) {
+              const int e = hl * E + i;
+              const bool desc = (e & k) == 0;
+              const uint32_t x = sv[i], y = sv[i + j];
+              const bool swp = desc ? (x < y) : (x > y);
+              sv[i] = swp ? y : x;
+              sv[i + j] = swp ? x : y;
+            }
+          }
+        }
+      }
+    }
+  } else {
+    // k <= 32: torch's 32-slot bitonic network on the gathered list. A slot pair
+    // (lower A, upper B) at stride st belongs to comparator thread
+    // tid = lower slot with bit st removed; stages of size 2..16 use the direction
+    // flag (tid & size/2) != 0, the final merge uses false. The pair exchanges when
+    // ((A > B and A valid) or B invalid) == flag, which also moves equal values.
+    uint32_t x = sv[0];
+    auto stage = [&](int size, int st, bool final_merge) {
+      const uint32_t o = (uint32_t)__shfl_xor((int)x, st, 64);
+      const bool lower = (hl & st) == 0;
+      const uint32_t A = lower ? x : o, B = lower ? o : x;
+      const int lo = lower ? hl : (hl ^ st);
+      const int tid = ((lo >> 1) & ~(st - 1)) | (lo & (st - 1));
+      const bool flag = final_merge ? false : ((tid & (size >> 1)) != 0);
+      const bool va = (A >> 15) & 1u, vb = (B >> 15) & 1u;
+      const bool sw = (((A >> 16) > (B >> 16)) && va) || !vb;
+      if (sw == flag) x = lower ? B : A;
+    };
+#pragma unroll
+    for (int size = 2; size < 32; size <<= 1)
+#pragma unroll
+      for (int st = size >> 1; st > 0; st >>= 1) stage(size, st, false);
+#pragma unroll
+    for (int st = 16; st > 0; st >>= 1) stage(32, st, true);
+    sv[0] = x;
+  }
+
+  if (t < p.S) {
+    int64_t* dst = p.out + ((int64_t)b * p.S + t) * p.K;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const uint32_t e = (uint32_t)(hl * E + i);
+      if (e < K) {
+        const uint32_t c = (E == 1) ? (sv[i] & 0x7fffu) : (0xffffu - (sv[i] & 0xffffu));
+        dst[e] = (p.causal && c >= (uint32_t)nv) ? (int64_t)-1 : (int64_t)c + p.offset;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int dsa_indexer_rope(void* q, const void* freqs_cis, int64_t b, int64_t s, int64_t h,
+                                int64_t d, int64_t rd, int32_t rope_mode, void* stream) {
+  if (b < 0 || s < 0 || h <= 0 || d <= 0 || rd <= 0 || rd > d || (rd & 1) || (d & 1))
+    return DSA_ERR_SHAPE;
+  if (rope_mode != DSA_ROPE_CPU && rope_mode != DSA_ROPE_TORCH_ROCM) return DSA_ERR_UNSUPPORTED;
+  if (b * s * h * d > (INT64_C(1) << 40)) return DSA_ERR_SHAPE;
+  if (b == 0 || s == 0) return DSA_OK;
+  if (!q || !freqs_cis) return DSA_ERR_NULL;
+  if (((uintptr_t)q & 3u) || ((uintptr_t)freqs_cis & 7u)) return DSA_ERR_ALIGN;
+  RopeParams p;
+  p.q = (uint16_t*)q;
+  p.freqs = (const float*)freqs_cis;
+  p.rows = b * s * h;
+  p.S = (int32_t)s;
+  p.H = (int32_t)h;
+  p.D = (int32_t)d;
+  p.rd = (int32_t)rd;
+  p.mode = rope_mode;
+  const int64_t n = p.rows * (rd / 2);
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
+  return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
+namespace {
+
+int launch_ix(const void* q, const void* kv_cache, int64_t kv_batch_stride, const void* wl,
+              float w_scale, const void* freqs_cis, int32_t rope_mode, int64_t* out,
+              uint16_t* scores, int64_t b, int64_t s, int64_t h, int64_t d, int64_t rd,
+              int64_t n_cand, int64_t k_out, int64_t ratio, int32_t causal, int64_t offset,
+              void* stream) {
+  if (b < 0 || s < 0 || h <= 0 || d <= 0 || n_cand < 1 || k_out < 1 || ratio < 1)
+    return DSA_ERR_SHAPE;
+  if (k_out > n_cand) return DSA_ERR_SHAPE;
+  if (h != kH || d != kD) return DSA_ERR_UNSUPPORTED;
+  if (n_cand > 2048 || k_out > 256) return DSA_ERR_UNSUPPORTED;
+  if (freqs_cis != nullptr) {
+    if (rd <= 0 || rd > d || (rd & 1)) return DSA_ERR_SHAPE;
+    if (rope_mode != DSA_ROPE_CPU && rope_mode != DSA_ROPE_TORCH_ROCM) return DSA_ERR_UNSUPPORTED;
+  }
+  if (kv_batch_stride < n_cand * d) return DSA_ERR_SHAPE;
+  if (b > (1 << 20) || s > (1 << 24)) return DSA_ERR_SHAPE;
+  if (b == 0 || s == 0) return DSA_OK;
+  if (!q || !kv_cache || !wl || (!out && !scores)) return DSA_ERR_NULL;
+  if (!dsa_host::aligned16(q) || !dsa_host::aligned16(kv_cache) || !dsa_host::aligned16(wl) ||
+      ((uintptr_t)out & 7u) || ((uintptr_t)scores & 1u) || (kv_batch_stride % 8) != 0 ||
+      (freqs_cis != nullptr && ((uintptr_t)freqs_cis & 7u)))
+    return DSA_ERR_ALIGN;
+
+  IxParams p;
+  p.q = (const uint16_t*)q;
+  p.kv = (const uint16_t*)kv_cache;
+  p.kvbs = kv_batch_stride;
+  p.wl = (const uint16_t*)wl;
+  p.wscale = w_scale;
+  p.freqs = (const float*)freqs_cis;
+  p.rope_mode = rope_mode;
+  p.out = out;
+  p.scores = scores;
+  p.B = (int32_t)b;
+  p.S = (int32_t)s;
+  p.rd = (int32_t)rd;
+  p.T = (int32_t)n_cand;
+  p.K = (int32_t)k_out;
+  p.ratio = (int32_t)(ratio > (1 << 30) ? (1 << 30) : ratio);
+  p.causal = causal ? 1 : 0;
+  p.offset = offset;
+  p.npairs = (int32_t)((s + 1) / 2);
+  const int ntile = (int)((n_cand + 31) / 32);
+  p.keys_bytes = ntile * 128;  // 2 halves x 32 lanes x uint16 per tile
+  int E = 1;
+  while (32 * E < k_out) E <<= 1;
+  p.wave_bytes = p.keys_bytes + 2048 + 8 * 32 * E;
+  const size_t smem = (size_t)p.wave_bytes * 4;
+  if (smem > 64 * 1024) return DSA_ERR_UNSUPPORTED;
+  const int64_t waves = (int64_t)b * p.npairs;
+  const int64_t blocks = (waves + 3) / 4;
+  hipStream_t st = (hipStream_t)stream;
+  switch (E) {
+    case 1: hipLaunchKernelGGL(ix_score_topk_kernel<1>, dim3((unsigned)blocks), dim3(256), smem, st, p); break;
+    case 2: hipLaunchKernelGGL(ix_score_topk_kernel<2>, dim3((unsigned)blocks), dim3(256), smem, st, p); break;
+    case 4: hipLaunchKernelGGL(ix_score_topk_kernel<4>, dim3((unsigned)blocks), dim3(256), smem, st, p); break;
+    case 8: hipLaunchKernelGGL(ix_score_topk_kernel<8>, dim3((unsigned)blocks), dim3(256), smem, st, p); break;
+    default: return DSA_ERR_UNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" int dsa_indexer_score_topk(const void* q, const void* kv_cache, int64_t kv_batch_stride,
+                                      const void* wl, float w_scale, const void* freqs_cis,
+                                      int32_t rope_mode, int64_t* out, int64_t b, int64_t s,
+                                      int64_t h, int64_t d, int64_t rd, int64_t n_cand,
+                                      int64_t k_out, int64_t ratio, int32_t causal,
+                                      int64_t offset, void* stream) {
+  if (out == nullptr && b > 0 && s > 0) return DSA_ERR_NULL;
+  return launch_ix(q, kv_cache, kv_batch_stride, wl, w_scale, freqs_cis, rope_mode, out, nullptr,
+                   b, s, h, d, rd, n_cand, k_out, ratio, causal, offset, stream);
+}
+
+extern "C" int dsa_indexer_scores(const void* q, const void* kv_cache, int64_t kv_batch_stride,
+                                  const void* wl, float w_scale, const void* freqs_cis,
+                                  int32_t rope_mode, void* scores, int64_t b, int64_t s, int64_t h,
+                                  int64_t d, int64_t rd, int64_t n_cand, int64_t ratio,
+                                  int32_t causal, void* stream) {
+  if (scores == nullptr && b > 0 && s > 0) return DSA_ERR_NULL;
+  return launch_ix(q, kv_cache, kv_batch_stride, wl, w_scale, freqs_cis, rope_mode, nullptr,
+                   (uint16_t*)scores, b, s, h, d, rd, n_cand, 1, ratio, causal, 0, stream);
+}

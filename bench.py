@@ -1,0 +1,227 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X DSA path; prints ONE JSON line.
+
+Headline (BASELINE.json metric, configs[1]): Task1 sparse attention at the full
+shape q[8,2600,64,128] bf16, kv[8,32,128], topk_idxs[8,2600,16] (drawn with
+replacement), inputs resident in HBM. One step = one forward call of the drop-in
+module (one kernel launch). value = algorithmic HBM bytes per call / time per call.
+
+Also reported (field "task2"): the Task2 indexer at configs[2] (full Model.forward =
+two torch projections + the fused score/top-k kernel), and the fused kernel alone.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
+
+# Algorithmic bytes of one Task1 call at configs[1]: q read + out write + kv + idx + sink.
+T1_SHAPE = dict(b=8, m=2600, h=64, d=128, n_kv=32, topk=16)
+
+
+def t1_bytes(b, m, h, d, n_kv, topk):
+    return 2 * (b * m * h * d) * 2 + b * n_kv * d * 2 + b * m * topk * 4 + h * 4
+
+
+# Task2 configs[2]: compulsory bytes of Model.forward (x, qr, kv_cache, weights, freqs, out)
+def t2_bytes(b=8, s=2600, dim=1024, ql=256, t=650, d=64, h=16, rd=32, k=128):
+    return (b * s * dim * 2 + b * s * ql * 2 + b * t * d * 2 + h * d * ql * 2 + h * dim * 2
+            + s * (rd // 2) * 8 + b * s * k * 8)
+
+
+def t2_kernel_bytes(b=8, s=2600, t=650, d=64, h=16, rd=32, k=128):
+    # fused kernel: q read (pre-RoPE), wl read, kv_cache, freqs rows, int64 output
+    return b * s * h * d * 2 + b * s * h * 2 + b * t * d * 2 + s * (rd // 2) * 8 + b * s * k * 8
+
+
+def _events_time(torch, fn, steps, stream):
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    stop.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per call
+
+
+def _cold_time(torch, fn, reps, stream, flush):
+    """ms per call with the 256 MB MALL flushed (512 MB written) before every call."""
+    ts = []
+    for _ in range(reps):
+        flush.fill_(1)
+        a = torch.cuda.Event(enable_timing=True)
+        z = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn()
+        z.record(stream)
+        z.synchronize()
+        ts.append(a.elapsed_time(z))
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def _traffic():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_task1_c2.json")
+    try:
+        with open(p) as f:
+            return json.load(f).get("traffic_bytes")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(torch, seconds_target=15.0):
+    """The oracle (torch restatement of reference/task1_v0_ref.py:5-24) on this host's CPU
+    cores, over a bounded sample of the configs[1] workload (one batch, a slice of tokens)."""
+    from oracle import sparse_attn as osa
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    g = torch.Generator().manual_seed(42)
+    m = 325  # 1/64 of the 20,800 tokens of configs[1]
+    q = torch.randn(1, m, 64, 128, generator=g).to(torch.bfloat16)
+    kv = torch.randn(1, 32, 128, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, 32, (1, m, 16), generator=g, dtype=torch.int32)
+    sink = torch.zeros(64)
+    osa.sparse_attn_ref(q, kv, sink, idx, 128 ** -0.5)  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds_target
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        osa.sparse_attn_ref(q, kv, sink, idx, 128 ** -0.5)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    times.sort()
+    sec = times[len(times) // 2]
+    nbytes = t1_bytes(1, m, 64, 128, 32, 16)
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        cpu = platform.processor() or "unknown"
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": ncores, "kind": "port",
+            "sample": f"1 of 8 batches x {m} of 2600 tokens (q[1,{m},64,128]), median of {len(times)} "
+                      f"runs of the oracle on {ncores} threads; {sec * 1e3:.1f} ms per sample; CPU {cpu}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-task2", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every config fits one MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from ascendc_kernel_amd import _native
+    from ascendc_kernel_amd import task1_sparse_attn as t1
+    from ascendc_kernel_amd import task2_indexer as t2
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    _native.load()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+
+    # ---------------- Task1 headline
+    torch.manual_seed(42)
+    q, kv, idx = [x.to(dev) for x in t1.get_inputs()]
+    model = t1.Model(*t1.get_init_inputs()).to(dev)
+    with torch.no_grad():
+        for _ in range(a.warmup):
+            model(q, kv, idx)
+        torch.cuda.synchronize()
+        ms = _events_time(torch, lambda: model(q, kv, idx), a.steps, stream)
+        torch.cuda.synchronize()
+        flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        ms_cold = _cold_time(torch, lambda: model(q, kv, idx), 10, stream, flush)
+        del flush
+    nb = t1_bytes(**T1_SHAPE)
+    gbps = nb / (ms * 1e-3) / 1e9
+
+    result = {
+        "metric": "µs/call + achieved HBM GB/s (% of peak), Task1 sparse-attn & Task2 indexer",
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_call": round(ms * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (torch.manual_seed(42), reference get_inputs distributions)",
+        "config": {"workload": "task1_sparse_attn configs[1]: q[8,2600,64,128] bf16, kv[8,32,128], "
+                               "topk_idxs[8,2600,16] int32 with replacement, attn_sink zeros",
+                   "algorithmic_bytes": nb, "kernel": "sa_mult_kernel (multiplicity, MFMA)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": _traffic()},
+        "cold_mall_us_per_call": round(ms_cold * 1e3, 2),
+    }
+
+    # ---------------- Task2
+    if not a.no_task2:
+        args = t2._make_args()
+        torch.manual_seed(42)
+        init = t2.get_init_inputs(device=dev)
+        m2 = t2.Model(*init).to(dev)
+        g = torch.Generator().manual_seed(5)
+        with torch.no_grad():
+            for p in (m2.wq_b.weight, m2.weights_proj.weight):
+                p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(torch.bfloat16))
+        x, qr, sp, off = t2.get_inputs(device=dev)
+        with torch.no_grad():
+            for _ in range(a.warmup):
+                m2(x, qr, sp, off)
+            torch.cuda.synchronize()
+            ms2 = _events_time(torch, lambda: m2(x, qr, sp, off), a.steps, stream)
+            qp = torch.nn.functional.linear(qr, m2.wq_b.weight).unflatten(-1, (16, 64)).contiguous()
+            wl = torch.nn.functional.linear(x, m2.weights_proj.weight)
+            fr = m2.freqs_cis[:2600]
+            scale = 64 ** -0.5 * 16 ** -0.5
+            kfn = lambda: _native.indexer_score_topk(qp, m2.kv_cache, wl, scale, fr, 32, 650, 128, 4, True, 0)
+            for _ in range(3):
+                kfn()
+            torch.cuda.synchronize()
+            msk = _events_time(torch, kfn, a.steps, stream)
+        kb = t2_kernel_bytes()
+        score_flop = 2 * 16 * 64 * sum(((t + 1) // 4) for t in range(2600)) * 8
+        result["task2"] = {
+            "workload": "task2_indexer configs[2]: x[8,2600,1024], qr[8,2600,256], kv_cache[8,650,64], "
+                        "W ~ N(0,0.02), top-128, causal, ratio 4",
+            "us_per_call": round(ms2 * 1e3, 2),
+            "model_bytes": t2_bytes(),
+            "model_GBps": round(t2_bytes() / (ms2 * 1e-3) / 1e9, 1),
+            "fused_kernel_us": round(msk * 1e3, 2),
+            "fused_kernel_GBps": round(kb / (msk * 1e-3) / 1e9, 1),
+            "fused_kernel_hbm_frac": round(kb / (msk * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "fused_kernel_useful_score_TFLOPs": round(score_flop / (msk * 1e-3) / 1e12, 2),
+            "fused_kernel_mfma_frac": round(score_flop / (msk * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 5),
+        }
+
+    if not a.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

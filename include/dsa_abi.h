@@ -1,0 +1,134 @@
+/*
+ * dsa_abi.h - C ABI of the MI355X (gfx950) DeepSeek-sparse-attention path.
+ *
+ * Two operators, each a drop-in for one of the reference's PyTorch modules:
+ *   Task1  sparse attention with attention sink      reference/task1_v0_ref.py:5-36
+ *   Task2  lightning indexer (RoPE, score, top-k)     reference/task2_v0_ref.py:93-144
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers (HBM) except where noted; the caller
+ *     owns every buffer. The library never allocates and keeps no state
+ *     between calls, so calls on different streams may run concurrently.
+ *   - Tensors are dense and row-major (C-contiguous) unless a stride argument
+ *     says otherwise. bf16 tensors are passed as raw 16-bit words.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). Launches
+ *     are asynchronous: a return value of DSA_OK means the work was enqueued.
+ *   - Every entry point returns DSA_OK (0) or a negative DSA_ERR_* code;
+ *     dsa_strerror() turns it into text. Shape checks run on the host before
+ *     anything is launched, so an error leaves all outputs untouched.
+ */
+#ifndef DSA_ABI_H_
+#define DSA_ABI_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSA_ABI_VERSION 1
+
+#define DSA_OK 0
+#define DSA_ERR_NULL (-1)        /* a required pointer is NULL */
+#define DSA_ERR_SHAPE (-2)       /* sizes are negative or inconsistent */
+#define DSA_ERR_UNSUPPORTED (-3) /* valid request this build does not implement */
+#define DSA_ERR_LAUNCH (-4)      /* the HIP runtime rejected a launch */
+#define DSA_ERR_DEVICE (-5)      /* no usable gfx950 device / attribute query failed */
+#define DSA_ERR_ALIGN (-6)       /* a pointer is not 16-byte aligned */
+
+/* Task1 kernel selection (the `variant` argument of dsa_sparse_attn_fwd). */
+#define DSA_SA_AUTO 0         /* multiplicity kernel when n_kv <= 32, else gather */
+#define DSA_SA_MULTIPLICITY 1 /* per-token kv-index histogram, all scores of a batch's kv block */
+#define DSA_SA_GATHER 2       /* gathers the topk rows of every token (any n_kv) */
+
+/* Rounding of the RoPE complex product (the `rope_mode` arguments). */
+#define DSA_ROPE_CPU 0        /* torch CPU: re = (a*c) - (b*d), im = (a*d) + (b*c), each product rounded */
+#define DSA_ROPE_TORCH_ROCM 1 /* torch-ROCm broadcast mul kernel: contraction depends on the unroll slot */
+
+int dsa_abi_version(void);
+const char* dsa_strerror(int code);
+
+/*
+ * Task1: out[b,m,h,:] = sum_t softmax_t(scale * q[b,m,h,:] . kv[b,idx_t,:] ; sink_h) kv[b,idx_t,:]
+ * where idx_t = topk_idxs[b,m,t] and the softmax denominator includes exp(sink_h - max).
+ *
+ * Replaces sparse_attn_ref (reference/task1_v0_ref.py:5-24), called from
+ * Model.forward (task1_v0_ref.py:35-36); on the Ascend side the same call is
+ * ModelNew.forward -> run_fused -> launch_sa_fused
+ * (src/task1_sparse_attn.py:746-804,420-429; src/sparse_attn_kernel_mm.asc:310-313).
+ *
+ *   q          bf16 [b, m, h, d]
+ *   kv         bf16 [b, n_kv, d]          shared K = V (MQA over the h heads)
+ *   topk_idxs  int32 [b, m, topk]         negative = masked slot (task1_v0_ref.py:8);
+ *                                         values >= n_kv are treated as masked
+ *   attn_sink  fp32 [h]
+ *   out        bf16 [b, m, h, d]
+ *   softmax_scale  fp32 value of the reference's head_dim ** -0.5
+ * Requirements: d == 128, h % 16 == 0, 1 <= n_kv, topk >= 1; the multiplicity
+ * variant also needs n_kv <= 32. q/kv/out 16-byte aligned.
+ */
+int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
+                        const float* attn_sink, void* out, int64_t b, int64_t m,
+                        int64_t h, int64_t d, int64_t n_kv, int64_t topk,
+                        float softmax_scale, int32_t variant, void* stream);
+
+/*
+ * Task2 RoPE, in place on the last `rd` channels of every head of q.
+ * Replaces apply_rotary_emb(q[..., -rd:], freqs_cis) (reference/task2_v0_ref.py:93-104,131)
+ * and the Ascend ix_rope launch (src/indexer_kernel_aiv.asc:19-111; src/task2_indexer.py:1117-1130).
+ *
+ *   q          bf16 [b, s, h, d], rotated channels are q[..., d-rd:] taken as (re, im) pairs
+ *   freqs_cis  complex64 [s, rd/2] as interleaved fp32 (re, im); row t is position start_pos + t,
+ *              i.e. the caller passes &freqs_cis[start_pos]
+ *   rope_mode  DSA_ROPE_CPU or DSA_ROPE_TORCH_ROCM (which torch rounding to reproduce)
+ * Requirements: rd even, 0 < rd <= d, d % 8 == 0.
+ */
+int dsa_indexer_rope(void* q, const void* freqs_cis, int64_t b, int64_t s, int64_t h,
+                     int64_t d, int64_t rd, int32_t rope_mode, void* stream);
+
+/*
+ * Task2 score + mask + top-k (the body of Model.forward after the two
+ * projections; reference/task2_v0_ref.py:131-143):
+ *   w[b,t,h]      = bf16(fp32(wl[b,t,h]) * w_scale)                          (:132)
+ *   S[b,t,h,k]    = bf16(q[b,t,h,:] . kv_cache[b,k,:])   fp32 accumulate      (:133)
+ *   score[b,t,k]  = bf16( sum_h bf16(relu(S) * w) )      fp32, torch order    (:134)
+ *   causal: score[b,t,k] = -inf for k >= (t+1)//ratio                         (:135-137)
+ *   out[b,t,:]    = indices of the k_out largest scores, value desc / index asc (:138)
+ *   causal: out = -1 where idx >= (t+1)//ratio, else idx + offset; non-causal: idx + offset (:139-143)
+ * Replaces the Ascend fused score/top-k kernel launch_ix_fused
+ * (src/indexer_kernel_mm.asc:421-436; src/task2_indexer.py:1338-1339).
+ *
+ *   q          bf16 [b, s, h, d]  projected queries (F.linear output). If `freqs_cis` is
+ *              not NULL the RoPE above is applied on the fly (q itself is not written),
+ *              which is equivalent to calling dsa_indexer_rope first.
+ *   kv_cache   bf16, row k of batch i at kv_cache + i*kv_batch_stride + k*d (elements)
+ *   wl         bf16 [b, s, h]      unscaled weights_proj output
+ *   out        int64 [b, s, k_out]
+ *   n_cand     number of candidate keys T = end_pos // ratio
+ *   causal     1 when start_pos == 0 (mask and -1 fill), else 0
+ * Requirements: h == 16, d == 64, rd as for dsa_indexer_rope (when freqs_cis != NULL),
+ * 1 <= n_cand <= 2048, 1 <= k_out <= min(n_cand, 256), ratio >= 1.
+ */
+int dsa_indexer_score_topk(const void* q, const void* kv_cache, int64_t kv_batch_stride,
+                           const void* wl, float w_scale, const void* freqs_cis,
+                           int32_t rope_mode, int64_t* out, int64_t b, int64_t s,
+                           int64_t h, int64_t d, int64_t rd, int64_t n_cand, int64_t k_out,
+                           int64_t ratio, int32_t causal, int64_t offset, void* stream);
+
+/*
+ * Task2 score stage alone: writes the bf16 index_score [b, s, n_cand] that the reference
+ * hands to topk (reference/task2_v0_ref.py:131-137), with masked entries = -inf in the
+ * causal case. Same arguments and requirements as dsa_indexer_score_topk; `scores` is a
+ * device buffer of b*s*n_cand bf16 words. Used to check the rounding chain stage by stage
+ * and by callers that want the scores themselves.
+ */
+int dsa_indexer_scores(const void* q, const void* kv_cache, int64_t kv_batch_stride,
+                       const void* wl, float w_scale, const void* freqs_cis, int32_t rope_mode,
+                       void* scores, int64_t b, int64_t s, int64_t h, int64_t d, int64_t rd,
+                       int64_t n_cand, int64_t ratio, int32_t causal, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_ABI_H_ */

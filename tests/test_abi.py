@@ -1,0 +1,100 @@
+"""The C-ABI library: loads, exports what include/dsa_abi.h declares, and rejects
+bad arguments on the host (these calls return before any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import REPO
+from ascendc_kernel_amd import _native
+
+
+def _declared():
+    text = open(os.path.join(REPO, "include", "dsa_abi.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(dsa_\w+)\s*\(", text, re.M)))
+
+
+def test_library_present_and_loads():
+    lib = _native.load()
+    assert lib.dsa_abi_version() == _native.ABI_VERSION
+
+
+def test_exports_every_declared_symbol():
+    decl = _declared()
+    assert set(decl) == set(_native.EXPORTS)
+    lib = ctypes.CDLL(_native.lib_path())
+    for name in decl:
+        assert hasattr(lib, name), name
+
+
+def test_strerror():
+    lib = _native.load()
+    assert lib.dsa_strerror(0) == b"ok"
+    for code in (-1, -2, -3, -4, -5, -6):
+        assert lib.dsa_strerror(code) not in (b"ok", b"unknown error")
+    assert lib.dsa_strerror(-99) == b"unknown error"
+
+
+def _sa(lib, **kw):
+    a = dict(q=16, kv=16, idx=16, sink=16, out=16, b=1, m=1, h=64, d=128, n_kv=32, topk=16,
+             scale=0.1, variant=0)
+    a.update(kw)
+    return lib.dsa_sparse_attn_fwd(a["q"], a["kv"], a["idx"], a["sink"], a["out"], a["b"], a["m"],
+                                   a["h"], a["d"], a["n_kv"], a["topk"], a["scale"], a["variant"], None)
+
+
+def test_sparse_attn_host_checks():
+    lib = _native.load()
+    assert _sa(lib, b=-1) == -2
+    assert _sa(lib, topk=0) == -2
+    assert _sa(lib, n_kv=0) == -2
+    assert _sa(lib, d=64) == -3
+    assert _sa(lib, h=24) == -3
+    assert _sa(lib, variant=1, n_kv=33) == -3
+    assert _sa(lib, variant=7) == -3
+    assert _sa(lib, b=0) == 0 and _sa(lib, m=0) == 0
+    assert _sa(lib, q=None) == -1
+    assert _sa(lib, out=None) == -1
+    assert _sa(lib, q=8) == -6
+
+
+def _ix(lib, **kw):
+    a = dict(q=16, kv=16, kvbs=650 * 64, wl=16, scale=0.03, fr=16, mode=1, out=16, b=1, s=8,
+             h=16, d=64, rd=32, T=650, K=128, ratio=4, causal=1, offset=0)
+    a.update(kw)
+    return lib.dsa_indexer_score_topk(a["q"], a["kv"], a["kvbs"], a["wl"], a["scale"], a["fr"],
+                                      a["mode"], a["out"], a["b"], a["s"], a["h"], a["d"], a["rd"],
+                                      a["T"], a["K"], a["ratio"], a["causal"], a["offset"], None)
+
+
+def test_indexer_host_checks():
+    lib = _native.load()
+    assert _ix(lib, K=700) == -2
+    assert _ix(lib, T=0) == -2
+    assert _ix(lib, ratio=0) == -2
+    assert _ix(lib, h=64) == -3
+    assert _ix(lib, d=128) == -3
+    assert _ix(lib, K=512) == -3
+    assert _ix(lib, mode=5) == -3
+    assert _ix(lib, rd=33) == -2
+    assert _ix(lib, kvbs=100) == -2
+    assert _ix(lib, s=0) == 0
+    assert _ix(lib, q=None) == -1
+    assert _ix(lib, wl=24) == -6
+
+
+def test_rope_host_checks():
+    lib = _native.load()
+    assert lib.dsa_indexer_rope(16, 16, 1, 4, 16, 64, 33, 1, None) == -2
+    assert lib.dsa_indexer_rope(16, 16, 1, 4, 16, 64, 80, 1, None) == -2
+    assert lib.dsa_indexer_rope(16, 16, 1, 4, 16, 64, 32, 3, None) == -3
+    assert lib.dsa_indexer_rope(16, 16, 0, 4, 16, 64, 32, 1, None) == 0
+    assert lib.dsa_indexer_rope(None, 16, 1, 4, 16, 64, 32, 1, None) == -1
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setenv("DSA_MI355X_LIB", str(tmp_path / "nope.so"))
+    with pytest.raises(RuntimeError, match="missing"):
+        _native.load()
