@@ -27,19 +27,31 @@ namespace {
 
 constexpr int kD = 128;
 
+// Streaming knobs (compile-time): cache policy of the q loads / out stores and
+// the number of resident waves the grid is sized for.
+#ifndef DSA_SA_NT_LOAD
+#define DSA_SA_NT_LOAD 1
+#endif
+#ifndef DSA_SA_NT_STORE
+#define DSA_SA_NT_STORE 1
+#endif
+#ifndef DSA_SA_TILES_PER_WAVE
+#define DSA_SA_TILES_PER_WAVE 4
+#endif
+
 struct MultParams {
   const uint16_t* q;
   const uint16_t* kv;
   const int32_t* idx;
   const float* sink;
   uint16_t* out;
-  int64_t M;  // tokens per batch
+  int64_t M;                 // tokens per batch
+  int64_t tiles_per_batch;   // M * H / 16
+  int64_t blocks_per_batch;  // ceil(tiles_per_batch / (4 * tiles per wave))
   int32_t H;
   int32_t NKV;
   int32_t TOPK;
   float scale;
-  int64_t total_tiles;
-  int64_t tiles_per_wave;
 };
 
 // Contraction permutation of the second product: logical k (lane group g owns
@@ -55,87 +67,145 @@ __device__ __forceinline__ int delta_ch(int mt, int i) {
   return 32 * (mt >> 1) + 8 * (i >> 2) + 4 * (mt & 1) + (i & 3);
 }
 
-__device__ __forceinline__ bf16x8 load_row16(const uint16_t* p) {
-  return __builtin_bit_cast(bf16x8, ld_nt(reinterpret_cast<const u32x4*>(p)));
+// Orders this wave's LDS accesses across lanes (LDS executes a wave's
+// instructions in order; this keeps the compiler from reordering them).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
 }
 
-__global__ __launch_bounds__(256) void sa_mult_kernel(MultParams p) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t t0 = wave * p.tiles_per_wave;
-  const int64_t t1 = t0 + p.tiles_per_wave < p.total_tiles ? t0 + p.tiles_per_wave : p.total_tiles;
-  if (t0 >= t1) return;
+__device__ __forceinline__ bf16x8 load_row16(const uint16_t* p) {
+#if DSA_SA_NT_LOAD
+  return __builtin_bit_cast(bf16x8, ld_nt(reinterpret_cast<const u32x4*>(p)));
+#else
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
+#endif
+}
 
+// One workgroup = 4 waves = 4 * TPW consecutive 16-row tiles of one batch.
+// Load order matters because vector-memory completions are counted in issue
+// order: the batch's kv block and the small per-tile values (sink, slot
+// indices) are requested first, then all q tiles of the wave; the workgroup
+// waits only for the first group, stages the kv block in LDS (as a swizzled
+// row copy and as the pre-permuted operand of the second product) and then
+// computes tile by tile while the q loads are still arriving.
+template <int TPW, bool BIGK>
+__global__ __launch_bounds__(256) void sa_mult_kernel(MultParams p) {
+  __shared__ u32x4 kraw[32 * 16];  // kv row r chunk c (8 channels) at r*16 + (c ^ (r & 15))
+  __shared__ u32x4 img_pv[8][64];  // fragment mt: kv[pi(8g+j)][delta(mt, n)], j = 0..7
+  __shared__ u32x4 obuf[4][256];   // per-wave output tile, 16 rows x 16 chunks, chunk ^ row
+  const int lane = threadIdx.x & 63;
+  const int wi = threadIdx.x >> 6;
   const int n = lane & 15;  // row of the tile (head h0 + n) = MFMA column
   const int g = lane >> 4;  // lane group: contraction slice 8g..8g+7
-  const int tpt = p.H >> 4; // 16-row tiles per token
+  const int b = (int)(blockIdx.x / p.blocks_per_batch);
+  const int64_t lt0 = ((blockIdx.x % p.blocks_per_batch) * 4 + wi) * TPW;  // first tile in batch b
+  const int tpt = p.H >> 4;  // 16-row tiles per token
+  const int64_t ntb = p.tiles_per_batch;
+  const bool live = lt0 < ntb;
+  const int nlive = live ? (int)((ntb - lt0) < TPW ? (ntb - lt0) : TPW) : 0;  // tiles of this wave
 
-  bf16x8 kqk[2][4];  // A operand of S^T: kv[16mt + n][32ks + 8g + j]
-  bf16x8 kpv[8];     // A operand of O^T: kv[pi(8g + j)][delta(mt, n)]
-  float cnt[8];      // multiplicities of kv rows 16mt + 4g + r (index mt*4 + r)
-  int cur_b = -1;
-  int64_t cur_tok = -1;
-
-  auto qaddr = [&](int64_t tile) -> const uint16_t* {
-    const int64_t tok = tile / tpt;
-    const int64_t row = tok * p.H + (tile - tok * tpt) * 16 + n;
-    return p.q + row * kD + 8 * g;
-  };
-
-  bf16x8 qv[4];
+  // Token and head block of each tile, from one division per wave. Dead tiles
+  // repeat the wave's last live tile so that every load below is unconditional
+  // (vector-memory waits are then exact counts of the loads issued later).
+  int64_t tok[TPW];
+  int h0[TPW];
   {
-    const uint16_t* a = qaddr(t0);
+    const int64_t first = live ? lt0 : ntb - 1;
+    int64_t tk = (int64_t)b * p.M + first / tpt;
+    int hh = (int)(first % tpt);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qv[ks] = load_row16(a + 32 * ks);
+    for (int i = 0; i < TPW; ++i) {
+      if (i > 0 && i < nlive) {
+        if (++hh == tpt) {
+          hh = 0;
+          ++tk;
+        }
+      }
+      tok[i] = tk;
+      h0[i] = hh * 16;
+    }
   }
 
-  for (int64_t tile = t0; tile < t1; ++tile) {
-    const int64_t tok = tile / tpt;
-    const int h0 = (int)(tile - tok * tpt) * 16;
-    const int b = (int)(tok / p.M);
-
-    if (b != cur_b) {
-      const uint16_t* kvb = p.kv + (int64_t)b * p.NKV * kD;
+  // 0. kv block of batch b: 32 rows x 16 chunks, two 16-byte chunks per thread.
+  const uint16_t* kvb = p.kv + (int64_t)b * p.NKV * kD;
+  u32x4 kr[2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int r = 16 * mt + n;
+  for (int j = 0; j < 2; ++j) {
+    const int e = threadIdx.x + 256 * j, r = e >> 4, c = e & 15;
+    const int rr = r < p.NKV ? r : p.NKV - 1;
+    kr[j] = *reinterpret_cast<const u32x4*>(kvb + (int64_t)rr * kD + 8 * c);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the issue order: kv, small values, q
+  // 1. sink of this lane's head per tile; slot indices of the wave's tokens
+  //    (token j of the wave is tok[0] + j; at most TPW of them).
+  float skv[TPW];
+  int idxv[TPW];
+  const int64_t tok_last = tok[TPW - 1];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          if (r < p.NKV) {
-            kqk[mt][ks] = __builtin_bit_cast(
-                bf16x8, *reinterpret_cast<const u32x4*>(kvb + (int64_t)r * kD + 32 * ks + 8 * g));
-          } else {
-            kqk[mt][ks] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-          }
-        }
+  for (int i = 0; i < TPW; ++i) {
+    skv[i] = p.sink[h0[i] + n];
+    const int64_t tj = tok[0] + i < tok_last ? tok[0] + i : tok_last;
+    idxv[i] = p.idx[tj * p.TOPK + (lane < p.TOPK ? lane : p.TOPK - 1)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 2. q loads of all this wave's tiles.
+  bf16x8 qv[TPW][4];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const uint16_t* a = p.q + (tok[i] * p.H + h0[i] + n) * kD + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qv[i][ks] = load_row16(a + 32 * ks);
+  }
+  // 3. stage kv in LDS (rows >= n_kv zero), then build the operand image of
+  //    the second product from it.
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = threadIdx.x + 256 * j, r = e >> 4, c = e & 15;
+    kraw[r * 16 + (c ^ (r & 15))] = (r < p.NKV) ? kr[j] : u32x4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+  {
+    const uint16_t* kh = reinterpret_cast<const uint16_t*>(kraw);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = threadIdx.x + 256 * j, f = e >> 6, ln = e & 63, nn = ln & 15, gg = ln >> 4;
+      const int ch = delta_ch(f, nn), cc = ch >> 3, ce = ch & 7;
+      u32x4 w;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int r0 = pi_kv(8 * gg + 2 * jj), r1 = pi_kv(8 * gg + 2 * jj + 1);
+        const uint32_t v0 = kh[(r0 * 16 + (cc ^ (r0 & 15))) * 8 + ce];
+        const uint32_t v1 = kh[(r1 * 16 + (cc ^ (r1 & 15))) * 8 + ce];
+        w[jj] = v0 | (v1 << 16);
       }
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        const int ch = delta_ch(mt, n);
-        uint16_t v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int r = pi_kv(8 * g + j);
-          v[j] = (r < p.NKV) ? kvb[(int64_t)r * kD + ch] : (uint16_t)0;
-        }
-        u32x4 w;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = (uint32_t)v[2 * j] | ((uint32_t)v[2 * j + 1] << 16);
-        kpv[mt] = __builtin_bit_cast(bf16x8, w);
-      }
-      cur_b = b;
+      img_pv[f][ln] = w;
     }
+  }
+  __syncthreads();
+  if (!live) return;
 
-    if (tok != cur_tok) {
+  float cnt[8];   // multiplicities of kv rows 16mt + 4g + r (index mt*4 + r)
+  bool used[8];   // cnt > 0
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    if (i >= nlive) break;
+    if (i == 0 || tok[i] != tok[i - 1]) {
       // Histogram of the token's slots over kv rows 0..31 with wave ballots;
       // each lane keeps the eight counts of the rows it owns in the S^T layout.
       int c[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) c[i] = 0;
-      const int32_t* ip = p.idx + tok * p.TOPK;
-      for (int c0 = 0; c0 < p.TOPK; c0 += 64) {
+      for (int k = 0; k < 8; ++k) c[k] = 0;
+      const int jt = (int)(tok[i] - tok[0]);
+      for (int c0 = 0; c0 < (BIGK ? p.TOPK : 1); c0 += 64) {
         int v = -1;
-        if (c0 + lane < p.TOPK) v = ip[c0 + lane];
+        if (c0 == 0) {
+#pragma unroll
+          for (int q = 0; q < TPW; ++q)
+            if (q == jt && lane < p.TOPK) v = idxv[q];
+        } else if (c0 + lane < p.TOPK) {  // only for topk > 64
+          v = p.idx[tok[i] * p.TOPK + c0 + lane];
+        }
         if (v >= p.NKV) v = -1;  // out-of-range slots are ignored (masked)
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
@@ -144,25 +214,19 @@ __global__ __launch_bounds__(256) void sa_mult_kernel(MultParams p) {
         }
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) cnt[i] = (float)c[i];
-      cur_tok = tok;
-    }
-
-    // Prefetch the next tile's q while this one is computed.
-    bf16x8 qn[4];
-    const bool has_next = tile + 1 < t1;
-    if (has_next) {
-      const uint16_t* a = qaddr(tile + 1);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qn[ks] = load_row16(a + 32 * ks);
+      for (int k = 0; k < 8; ++k) {
+        cnt[k] = (float)c[k];
+        used[k] = c[k] > 0;
+      }
     }
 
     // S^T tiles: kv rows 0..15 and 16..31 against the 16 rows of this tile.
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      s0 = mfma16x16x32(kqk[0][ks], qv[ks], s0);
-      s1 = mfma16x16x32(kqk[1][ks], qv[ks], s1);
+      // A operand: chunk 4ks+g of kv row 16mt+n (row & 15 == n)
+      s0 = mfma16x16x32(__builtin_bit_cast(bf16x8, kraw[n * 16 + ((4 * ks + g) ^ n)]), qv[i][ks], s0);
+      s1 = mfma16x16x32(__builtin_bit_cast(bf16x8, kraw[(16 + n) * 16 + ((4 * ks + g) ^ n)]), qv[i][ks], s1);
     }
     float sv[8];
 #pragma unroll
@@ -172,23 +236,24 @@ __global__ __launch_bounds__(256) void sa_mult_kernel(MultParams p) {
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (cnt[i] > 0.f) mx = fmaxf(mx, sv[i]);
+    for (int k = 0; k < 8; ++k)
+      if (used[k]) mx = fmaxf(mx, sv[k]);
     mx = fmaxf(mx, shfl_xor_f(mx, 16));
     mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    const float sk = p.sink[h0 + n];
+    const float sk = skv[i];
+    const int64_t tk = tok[i];
     const float mrow = fmaxf(mx, sk);
     float e[8];
     float z = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      e[i] = (cnt[i] > 0.f) ? __expf(sv[i] - mrow) * cnt[i] : 0.f;
-      z += e[i];
+    for (int k = 0; k < 8; ++k) {
+      e[k] = used[k] ? __expf(sv[k] - mrow) * cnt[k] : 0.f;
+      z += e[k];
     }
     z += shfl_xor_f(z, 16);
     z += shfl_xor_f(z, 32);
     z += __expf(sk - mrow);
-    const float rz = 1.0f / z;
+    const float rz = __builtin_amdgcn_rcpf(z);
     u32x4 whi, wlo;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -204,27 +269,35 @@ __global__ __launch_bounds__(256) void sa_mult_kernel(MultParams p) {
     f32x4 o[8];
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
-      o[mt] = mfma16x16x32(kpv[mt], plo, f32x4{0.f, 0.f, 0.f, 0.f});
-      o[mt] = mfma16x16x32(kpv[mt], phi, o[mt]);
+      const bf16x8 a = __builtin_bit_cast(bf16x8, img_pv[mt][lane]);
+      o[mt] = mfma16x16x32(a, plo, f32x4{0.f, 0.f, 0.f, 0.f});
+      o[mt] = mfma16x16x32(a, phi, o[mt]);
     }
-    {
-      const int64_t row = tok * p.H + h0 + n;
-      uint16_t* dst = p.out + row * kD + 8 * g;
+    // Transpose the tile through LDS so every store instruction writes four
+    // whole 256-byte rows (1 KB contiguous) instead of 16 rows x 64 bytes.
+    u32x4* ob = obuf[wi];
 #pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        u32x4 w;
-        w[0] = pack_bf2(o[2 * pp][0], o[2 * pp][1]);
-        w[1] = pack_bf2(o[2 * pp][2], o[2 * pp][3]);
-        w[2] = pack_bf2(o[2 * pp + 1][0], o[2 * pp + 1][1]);
-        w[3] = pack_bf2(o[2 * pp + 1][2], o[2 * pp + 1][3]);
-        st_nt(reinterpret_cast<u32x4*>(dst + 32 * pp), w);
-      }
+    for (int pp = 0; pp < 4; ++pp) {
+      u32x4 w;
+      w[0] = pack_bf2(o[2 * pp][0], o[2 * pp][1]);
+      w[1] = pack_bf2(o[2 * pp][2], o[2 * pp][3]);
+      w[2] = pack_bf2(o[2 * pp + 1][0], o[2 * pp + 1][1]);
+      w[3] = pack_bf2(o[2 * pp + 1][2], o[2 * pp + 1][3]);
+      ob[n * 16 + ((4 * pp + g) ^ n)] = w;  // chunk 4pp+g of row n
     }
-
-    if (has_next) {
+    wave_lds_sync();
+    u32x4* dst = reinterpret_cast<u32x4*>(p.out + (tk * p.H + h0[i]) * kD);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qv[ks] = qn[ks];
+    for (int k = 0; k < 4; ++k) {
+      const int r = 4 * k + (lane >> 4), c = lane & 15;
+      const u32x4 w = ob[r * 16 + (c ^ r)];
+#if DSA_SA_NT_STORE
+      st_nt(dst + r * 16 + c, w);
+#else
+      dst[r * 16 + c] = w;
+#endif
     }
+    wave_lds_sync();
   }
 }
 
@@ -286,9 +359,6 @@ extern "C" int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t*
     return dsa_sparse_attn_gather_launch(q, kv, topk_idxs, attn_sink, out, b, m, h, n_kv, topk,
                                          softmax_scale, s);
 
-  int cu = 0;
-  int rc = dsa_host::device_cu_count(&cu);
-  if (rc != DSA_OK) return rc;
   MultParams p;
   p.q = (const uint16_t*)q;
   p.kv = (const uint16_t*)kv;
@@ -300,11 +370,14 @@ extern "C" int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t*
   p.NKV = (int32_t)n_kv;
   p.TOPK = (int32_t)topk;
   p.scale = softmax_scale;
-  p.total_tiles = b * m * (h / 16);
-  const int64_t waves = (int64_t)cu * 16;
-  p.tiles_per_wave = (p.total_tiles + waves - 1) / waves;
-  const int64_t used_waves = (p.total_tiles + p.tiles_per_wave - 1) / p.tiles_per_wave;
-  const int64_t blocks = (used_waves + 3) / 4;
-  hipLaunchKernelGGL(sa_mult_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
+  p.tiles_per_batch = m * (h / 16);
+  constexpr int tiles_per_block = 4 * DSA_SA_TILES_PER_WAVE;
+  p.blocks_per_batch = (p.tiles_per_batch + tiles_per_block - 1) / tiles_per_block;
+  const int64_t blocks = b * p.blocks_per_batch;
+  if (blocks > INT32_MAX) return DSA_ERR_SHAPE;
+  if (topk <= 64)
+    hipLaunchKernelGGL((sa_mult_kernel<DSA_SA_TILES_PER_WAVE, false>), dim3((unsigned)blocks), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((sa_mult_kernel<DSA_SA_TILES_PER_WAVE, true>), dim3((unsigned)blocks), dim3(256), 0, s, p);
   return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
 }
