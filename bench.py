@@ -121,6 +121,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-task2", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run 5 plain device copies of 256 MiB (counter calibration for rocprofv3 --pmc)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -155,6 +157,13 @@ def main():
         del flush
     nb = t1_bytes(**T1_SHAPE)
     gbps = nb / (ms * 1e-3) / 1e9
+    if a.calib_copy:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     result = {
         "metric": "µs/call + achieved HBM GB/s (% of peak), Task1 sparse-attn & Task2 indexer",
