@@ -86,14 +86,17 @@ def get_init_inputs(n_heads=64, head_dim=128):
     return [n_heads, head_dim]
 
 
-def gather_inputs(b, m, h, d, n_kv, topk, generator=None):
-    """C4-style inputs: per token t, min(t+1, topk) distinct indices from [0, t], rest -1."""
-    q = torch.randn(b, m, h, d, generator=generator).to(torch.bfloat16)
-    kv = torch.randn(b, n_kv, d, generator=generator).to(torch.bfloat16)
-    idx = torch.full((b, m, topk), -1, dtype=torch.int32)
-    for t in range(m):
-        n = min(t + 1, topk, n_kv)
-        for bi in range(b):
-            perm = torch.randperm(min(t + 1, n_kv), generator=generator)[:n]
-            idx[bi, t, :n] = perm.to(torch.int32)
-    return q, kv, idx
+def gather_inputs(b, m, h, d, n_kv, topk, generator=None, device="cpu"):
+    """configs[3]-style inputs: token t selects min(t+1, topk) distinct rows of [0, t]
+    (random order), remaining slots -1 (the reference's masked marker)."""
+    q = torch.randn(b, m, h, d, generator=generator).to(torch.bfloat16).to(device)
+    kv = torch.randn(b, n_kv, d, generator=generator).to(torch.bfloat16).to(device)
+    idx = torch.empty(b, m, topk, dtype=torch.int32)
+    cols = torch.arange(n_kv)
+    for t0 in range(0, m, 256):
+        t = torch.arange(t0, min(m, t0 + 256))
+        sc = torch.rand(b, len(t), n_kv, generator=generator)
+        sc = sc.masked_fill(cols[None, None, :] > t[None, :, None], -1.0)
+        val, ix = sc.topk(topk, dim=-1)
+        idx[:, t0:t0 + len(t)] = torch.where(val >= 0, ix, torch.full_like(ix, -1)).to(torch.int32)
+    return q, kv, idx.to(device)

@@ -153,3 +153,51 @@ def test_fixture_masked_needs_gather_variant(gpu):
         assert e.code == -3
         pytest.skip("gather variant not built yet")
     _compare(out.cpu(), bf16_from_bits(f["out"]), "masked-fixture")
+
+
+GATHER_CASES = [
+    # b, m, h, n_kv, topk, seed, masked, sink
+    (1, 40, 64, 48, 24, 21, 0.2, 1.0),
+    (2, 37, 32, 300, 100, 22, 0.1, 0.0),
+    (1, 9, 16, 64, 33, 23, 0.0, 2.0),
+    (2, 16, 48, 128, 64, 24, 0.3, -1.0),
+    (1, 5, 128, 1000, 2048, 25, 0.5, 0.5),
+    (1, 3, 64, 40, 1, 26, 0.0, 0.0),
+]
+
+
+@pytest.mark.parametrize("case", GATHER_CASES)
+def test_gather_shapes_and_masks(gpu, case):
+    b, m, h, n_kv, topk, seed, masked, sink_scale = case
+    _say("gather case", case)
+    q, kv, idx, sink = _case(b, m, h, n_kv, topk, seed, masked, sink_scale)
+    out = _native.sparse_attn_fwd(q, kv, idx, sink, 128 ** -0.5, _native.DSA_SA_GATHER)
+    ref = osa.sparse_attn_ref(q, kv, sink, idx, 128 ** -0.5)
+    _compare(out, ref, f"gather{case}")
+
+
+def test_gather_equals_multiplicity(gpu):
+    """Both variants on the same small-n_kv inputs (duplicates included)."""
+    q, kv, idx, sink = _case(2, 64, 64, 32, 16, 27, 0.2, 0.8)
+    _say("gather vs multiplicity")
+    a = _native.sparse_attn_fwd(q, kv, idx, sink, 128 ** -0.5, _native.DSA_SA_GATHER)
+    b_ = _native.sparse_attn_fwd(q, kv, idx, sink, 128 ** -0.5, _native.DSA_SA_MULTIPLICITY)
+    ref = osa.sparse_attn_ref(q, kv, sink, idx, 128 ** -0.5)
+    _compare(a, ref, "gather-small")
+    _compare(b_, ref, "mult-small")
+
+
+def test_full_shape_c4_gather(gpu):
+    """q[4,4096,64,128], kv[4,8192,128], topk 512 drawn from [0, t], -1 padded."""
+    g = torch.Generator().manual_seed(42)
+    _say("case c4 inputs")
+    q, kv, idx = osa.gather_inputs(4, 4096, 64, 128, 8192, 512, generator=g, device=gpu)
+    sink = torch.zeros(64, device=gpu)
+    _say("case c4 kernel")
+    out = _native.sparse_attn_fwd(q, kv, idx, sink, 128 ** -0.5)
+    torch.cuda.synchronize()
+    _say("case c4 oracle")
+    ref = torch.cat([osa.sparse_attn_ref(q[:, i:i + 512], kv, sink, idx[:, i:i + 512], 128 ** -0.5)
+                     for i in range(0, 4096, 512)], dim=1)
+    exact = _compare(out, ref, "c4")
+    assert exact > 0.97
