@@ -60,3 +60,23 @@ def get_inputs():
 
 def get_init_inputs():
     return [n_heads, head_dim]
+
+
+def get_gather_inputs(batch_size=4, seq_len=4096, n_kv=8192, topk=512, device="cuda", seed=42):
+    """configs[3] (true-gather) inputs, built on `device`: q [b, m, 64, 128] and
+    kv [b, n_kv, 128] bf16 ~N(0,1); token t selects min(t+1, topk) distinct rows of
+    the causally visible range [0, t] in random order, the remaining slots are -1
+    (the reference's masked marker, task1_v0_ref.py:8)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(batch_size, seq_len, n_heads, head_dim, generator=g, device=device).to(torch.bfloat16)
+    kv = torch.randn(batch_size, n_kv, head_dim, generator=g, device=device).to(torch.bfloat16)
+    idx = torch.empty(batch_size, seq_len, topk, dtype=torch.int32, device=device)
+    cols = torch.arange(n_kv, device=device)
+    step = 256
+    for t0 in range(0, seq_len, step):
+        t = torch.arange(t0, min(seq_len, t0 + step), device=device)
+        sc = torch.rand(batch_size, len(t), n_kv, generator=g, device=device)
+        sc = sc.masked_fill(cols[None, None, :] > t[None, :, None], -1.0)
+        val, ix = sc.topk(topk, dim=-1)
+        idx[:, t0:t0 + len(t)] = torch.where(val >= 0, ix, torch.full_like(ix, -1)).to(torch.int32)
+    return [q, kv, idx]

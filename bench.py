@@ -6,8 +6,10 @@ shape q[8,2600,64,128] bf16, kv[8,32,128], topk_idxs[8,2600,16] (drawn with
 replacement), inputs resident in HBM. One step = one forward call of the drop-in
 module (one kernel launch). value = algorithmic HBM bytes per call / time per call.
 
-Also reported (field "task2"): the Task2 indexer at configs[2] (full Model.forward =
-two torch projections + the fused score/top-k kernel), and the fused kernel alone.
+Also reported: "task1_c4", the true-gather kernel at configs[3] (MFMA-bound: useful
+TFLOP/s and fraction of the dense bf16 peak), and "task2", the Task2 indexer at
+configs[2] (full Model.forward = two torch projections + the fused score/top-k
+kernel) and the fused kernel alone.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10]
 """
@@ -69,13 +71,13 @@ def _cold_time(torch, fn, reps, stream, flush):
     return ts[len(ts) // 2]
 
 
-def _traffic():
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
-    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_task1_c2.json")
+def _traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary, if present."""
+    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
         with open(p) as f:
-            return json.load(f).get("traffic_bytes")
-    except (OSError, ValueError):
+            return json.load(f)["kernels"][kernel]["traffic_bytes"]
+    except (OSError, ValueError, KeyError):
         return None
 
 
@@ -121,6 +123,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-task2", action="store_true")
+    ap.add_argument("--no-c4", action="store_true", help="skip the configs[3] true-gather leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run 5 plain device copies of 256 MiB (counter calibration for rocprofv3 --pmc)")
     a = ap.parse_args()
@@ -183,9 +186,37 @@ def main():
                                "topk_idxs[8,2600,16] int32 with replacement, attn_sink zeros",
                    "algorithmic_bytes": nb, "kernel": "sa_mult_kernel (multiplicity, MFMA)"},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": _traffic()},
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": _traffic("sa_mult_kernel")},
         "cold_mall_us_per_call": round(ms_cold * 1e3, 2),
     }
+
+    # ---------------- Task1 true-gather
+    if not a.no_c4:
+        torch.cuda.empty_cache()
+        q4, kv4, idx4 = t1.get_gather_inputs(device=dev)
+        m4 = t1.Model(64, 128).to(dev)
+        with torch.no_grad():
+            for _ in range(3):
+                m4(q4, kv4, idx4)
+            torch.cuda.synchronize()
+            ms4 = _events_time(torch, lambda: m4(q4, kv4, idx4), max(5, a.steps // 5), stream)
+        valid = int((idx4 >= 0).sum().item())
+        flop4 = 4 * 64 * 128 * valid          # QK + PV over the valid slots
+        b4 = t1_bytes(4, 4096, 64, 128, 8192, 512)
+        result["task1_c4"] = {
+            "workload": "task1 configs[3]: q[4,4096,64,128] bf16, kv[4,8192,128], topk 512 distinct "
+                        "of [0,t], -1 padded",
+            "kernel": "sa_gather_kernel",
+            "us_per_call": round(ms4 * 1e3, 2),
+            "valid_slot_frac": round(valid / idx4.numel(), 4),
+            "useful_TFLOPs": round(flop4 / (ms4 * 1e-3) / 1e12, 1),
+            "mfma_frac": round(flop4 / (ms4 * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "issued_mfma_TFLOPs": round(1.5 * flop4 / (ms4 * 1e-3) / 1e12, 1),
+            "algorithmic_bytes": b4,
+            "GBps": round(b4 / (ms4 * 1e-3) / 1e9, 1),
+            "traffic": _traffic("sa_gather_kernel"),
+        }
+        del q4, kv4, idx4
 
     # ---------------- Task2
     if not a.no_task2:
@@ -225,6 +256,7 @@ def main():
             "fused_kernel_hbm_frac": round(kb / (msk * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
             "fused_kernel_useful_score_TFLOPs": round(score_flop / (msk * 1e-3) / 1e12, 2),
             "fused_kernel_mfma_frac": round(score_flop / (msk * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 5),
+            "fused_kernel_traffic": _traffic("ix_score_topk_kernel"),
         }
 
     if not a.no_cpu:
