@@ -65,7 +65,8 @@ const char* dsa_strerror(int code);
  *   out        bf16 [b, m, h, d]
  *   softmax_scale  fp32 value of the reference's head_dim ** -0.5
  * Requirements: d == 128, h % 16 == 0, 1 <= n_kv, topk >= 1; the multiplicity
- * variant also needs n_kv <= 32. q/kv/out 16-byte aligned.
+ * variant also needs n_kv <= 32, the gather variant h <= 128, topk <= 2048,
+ * n_kv <= 2^23 and softmax_scale > 0. q/kv/out 16-byte aligned.
  */
 int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
                         const float* attn_sink, void* out, int64_t b, int64_t m,
