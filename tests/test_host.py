@@ -76,3 +76,22 @@ def test_task2_args_match_reference_config():
     a = t2._make_args()
     assert (a.dim, a.index_n_heads, a.index_head_dim, a.index_topk, a.q_lora_rank, a.rope_head_dim,
             a.max_seq_len, a.max_batch_size) == (1024, 16, 64, 128, 256, 32, 2600, 8)
+
+
+def test_task1_gather_inputs_properties():
+    """configs[3] input builders: token t holds min(t+1, topk) distinct rows of [0, t], rest -1."""
+    from oracle import sparse_attn as osa
+    g = torch.Generator().manual_seed(3)
+    built = [t1.get_gather_inputs(batch_size=2, seq_len=70, n_kv=96, topk=40, device="cpu", seed=5),
+             list(osa.gather_inputs(2, 70, 64, 128, 96, 40, generator=g))]
+    for q, kv, idx in built:
+        assert idx.dtype == torch.int32 and tuple(idx.shape) == (2, 70, 40)
+        assert q.dtype == torch.bfloat16 and kv.dtype == torch.bfloat16
+        for b in range(2):
+            for t in range(70):
+                row = idx[b, t]
+                n = min(t + 1, 40)
+                valid = row[:n]
+                assert bool((valid >= 0).all()) and bool((valid <= t).all())
+                assert len(set(valid.tolist())) == n
+                assert bool((row[n:] == -1).all())
