@@ -48,6 +48,27 @@ __device__ __forceinline__ void st_nt(T* p, T v) {
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// One complex product of RoPE in the rounding torch uses.
+//  DSA_ROPE_CPU: vectorised CPU kernel, every product rounded, no FMA.
+//  DSA_ROPE_TORCH_ROCM: the broadcast elementwise kernel of torch-ROCm; its
+//  unrolled loop contracts unroll slots 0..2 as re = fma(a, c, -(b*d)),
+//  im = fma(b, c, a*d) and slot 3 as re = fma(-b, d, a*c), im = (a*d) + (b*c),
+//  where slot = (n / 128) % 4 for the flat index n of the complex element in the
+//  [b, s, h, rd/2] tensor (measured: 1.33 M of 1.33 M elements agree bit for bit).
+__device__ __forceinline__ void rope_pair(float a, float b, float c, float d, int mode,
+                                          int64_t n, float& re, float& im) {
+  if (mode == DSA_ROPE_CPU) {
+    re = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, d));
+    im = __fadd_rn(__fmul_rn(a, d), __fmul_rn(b, c));
+  } else if (((n >> 7) & 3) != 3) {
+    re = __fmaf_rn(a, c, -__fmul_rn(b, d));
+    im = __fmaf_rn(b, c, __fmul_rn(a, d));
+  } else {
+    re = __fmaf_rn(-b, d, __fmul_rn(a, c));
+    im = __fadd_rn(__fmul_rn(a, d), __fmul_rn(b, c));
+  }
+}
+
 }  // namespace dsa
 
 // Host helpers shared by the entry points.

@@ -34,27 +34,6 @@ namespace {
 constexpr int kH = 16;  // index heads handled by the fused kernel
 constexpr int kD = 64;  // index head dim handled by the fused kernel
 
-// One complex product of RoPE in the rounding torch uses.
-//  DSA_ROPE_CPU: vectorised CPU kernel, every product rounded, no FMA.
-//  DSA_ROPE_TORCH_ROCM: the broadcast elementwise kernel of torch-ROCm; its
-//  unrolled loop contracts unroll slots 0..2 as re = fma(a, c, -(b*d)),
-//  im = fma(b, c, a*d) and slot 3 as re = fma(-b, d, a*c), im = (a*d) + (b*c),
-//  where slot = (n / 128) % 4 for the flat index n of the complex element in the
-//  [b, s, h, rd/2] tensor (measured: 1.33 M of 1.33 M elements agree bit for bit).
-__device__ __forceinline__ void rope_pair(float a, float b, float c, float d, int mode,
-                                          int64_t n, float& re, float& im) {
-  if (mode == DSA_ROPE_CPU) {
-    re = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, d));
-    im = __fadd_rn(__fmul_rn(a, d), __fmul_rn(b, c));
-  } else if (((n >> 7) & 3) != 3) {
-    re = __fmaf_rn(a, c, -__fmul_rn(b, d));
-    im = __fmaf_rn(b, c, __fmul_rn(a, d));
-  } else {
-    re = __fmaf_rn(-b, d, __fmul_rn(a, c));
-    im = __fadd_rn(__fmul_rn(a, d), __fmul_rn(b, c));
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Standalone in-place RoPE: one thread per complex pair.
 struct RopeParams {
@@ -479,6 +458,12 @@ extern "C" int dsa_indexer_rope(void* q, const void* freqs_cis, int64_t b, int64
   return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
 }
 
+int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batch_stride,
+                            const void* wl, float w_scale, const void* freqs_cis,
+                            int32_t rope_mode, int64_t* out, uint16_t* scores, int64_t b,
+                            int64_t s, int64_t rd, int64_t n_cand, int64_t k_out,
+                            int64_t ratio, int32_t causal, int64_t offset, hipStream_t stream);
+
 namespace {
 
 int launch_ix(const void* q, const void* kv_cache, int64_t kv_batch_stride, const void* wl,
@@ -489,8 +474,9 @@ int launch_ix(const void* q, const void* kv_cache, int64_t kv_batch_stride, cons
   if (b < 0 || s < 0 || h <= 0 || d <= 0 || n_cand < 1 || k_out < 1 || ratio < 1)
     return DSA_ERR_SHAPE;
   if (k_out > n_cand) return DSA_ERR_SHAPE;
-  if (h != kH || d != kD) return DSA_ERR_UNSUPPORTED;
-  if (n_cand > 2048 || k_out > 256) return DSA_ERR_UNSUPPORTED;
+  const bool wide = (h == 64 && d == 128);
+  if (!wide && (h != kH || d != kD)) return DSA_ERR_UNSUPPORTED;
+  if (!wide && (n_cand > 2048 || k_out > 256)) return DSA_ERR_UNSUPPORTED;
   if (freqs_cis != nullptr) {
     if (rd <= 0 || rd > d || (rd & 1)) return DSA_ERR_SHAPE;
     if (rope_mode != DSA_ROPE_CPU && rope_mode != DSA_ROPE_TORCH_ROCM) return DSA_ERR_UNSUPPORTED;
@@ -503,6 +489,11 @@ int launch_ix(const void* q, const void* kv_cache, int64_t kv_batch_stride, cons
       ((uintptr_t)out & 7u) || ((uintptr_t)scores & 1u) || (kv_batch_stride % 8) != 0 ||
       (freqs_cis != nullptr && ((uintptr_t)freqs_cis & 7u)))
     return DSA_ERR_ALIGN;
+
+  if (wide)
+    return dsa_indexer_wide_launch(q, kv_cache, kv_batch_stride, wl, w_scale, freqs_cis, rope_mode,
+                                   out, scores, b, s, rd, n_cand, k_out, ratio, causal, offset,
+                                   (hipStream_t)stream);
 
   IxParams p;
   p.q = (const uint16_t*)q;

@@ -1,0 +1,441 @@
+// Task2 lightning indexer, wide configuration: 64 index heads x 128 channels,
+// up to 8192 candidates, top-k up to 2048 (the DSA layer of DeepSeek-V3.2).
+//
+// Semantics are those of Model.forward of reference/task2_v0_ref.py:123-144
+// after the two projections, with the rounding torch-ROCm applies at these
+// shapes (established on the MI355X with planted inputs):
+//   RoPE  (:131)  as in the 16-head kernel (rope_pair, slot rule on the flat index)
+//   w     (:132)  bf16(fp32(wl) * fp32(scale))
+//   S     (:133)  bf16(q . k), fp32 accumulation over channels 0..127 in order
+//   score (:134)  bf16(sum_h bf16(relu(S_h) * w_h)), fp32 sum in the order of
+//                 torch's reduction kernel for a 64-long middle dimension when the
+//                 candidate count is a multiple of 4: two threads take the even and
+//                 the odd heads; each keeps four accumulators over its heads
+//                 (accumulator i of thread y gets heads y + 2i + 8m, m = 0..7, in
+//                 order) combined as ((a0 + a1) + a2) + a3; then even + odd.
+//   mask / top-k / fill (:135-143) as in the 16-head kernel; ties by index.
+//
+// Workgroup = 4 consecutive tokens x 2 waves (even heads, odd heads). The
+// candidates go in tiles of 32 keys (8 KB), copied into a 4-buffer LDS ring by
+// buffer_load ... lds and shared by the 8 waves. A wave computes
+//   S[32 heads x 32 candidates] = Q[32 x 128] . K^T   (8 x mfma 32x32x16)
+// with its 32 head rows permuted so that every lane holds, for one candidate,
+// 2 of its thread's 4 accumulators complete (8 heads each, in order): the
+// relu/w/bf16 chain and the sums are lane-local (v_dot2 on packed bf16 pairs
+// does the exact products and the fp32 additions), one v_permlane32_swap joins
+// the lane halves, and the even/odd totals meet in LDS. Scores become 16-bit
+// order keys in LDS; per token a two-pass 8-bit radix select finds the k-th key,
+// the picks are compacted ([> k-th] then [== k-th] in index order) and
+// bitonic-sorted on (key, ~index) before the int64 indices are written.
+#include "dsa_common.h"
+
+using namespace dsa;
+
+namespace {
+
+constexpr int kWH = 64;      // index heads
+constexpr int kWD = 128;     // channels per head
+constexpr int kTok = 4;      // tokens per workgroup
+constexpr int kTileC = 32;   // candidates per tile
+constexpr int kRingW = 4;    // LDS tile buffers
+constexpr int kMaxT = 8192;
+constexpr int kMaxK = 2048;
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef short s16v2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+struct WideParams {
+  const uint16_t* q;    // [B, S, 64, 128] projected queries (before RoPE)
+  const uint16_t* kv;   // row k of batch b at kv + b*kvbs + k*128
+  int64_t kvbs;
+  const uint16_t* wl;   // [B, S, 64]
+  float wscale;
+  const float* freqs;   // [S, rd/2, 2] (rows from start_pos) or nullptr
+  int32_t rope_mode;
+  int64_t* out;         // [B, S, K]
+  uint16_t* scores;     // optional [B, S, T] bf16 score dump (masked -inf); then no top-k
+  int32_t B, S, rd, T, K, ratio, causal;
+  int64_t offset;
+  int32_t groups;       // ceil(S / kTok)
+  int32_t tpad;         // key row length in LDS (T rounded up to 32)
+  int32_t psort;        // power of two >= K (bitonic size)
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Raw buffer resource: base, stride 0, num_records = bytes (reads at or beyond
+// read zero), gfx9 raw-buffer format word.
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return i32x4{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a),
+               __builtin_amdgcn_readfirstlane((int32_t)((a >> 32) & 0xffffu)), (int32_t)bytes,
+               0x00020000};
+}
+
+// buffer_load_dwordx4 ... lds: lane l copies 16 B at byte offset voff to LDS
+// address m0 + 16 l. From inline asm so that the compiler does not track it
+// (it would put a vmcnt(0) before every LDS read); waited with wait_vmcnt.
+__device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t voff, uint32_t m0) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "{m0}"(m0)
+               : "memory");
+}
+
+__device__ __forceinline__ int swz(int r, int c) { return r * 16 + (c ^ (r & 15)); }
+
+// Head of MFMA row R in the wave for head parity y: lane half hf = (R/4)%2 and
+// register r = 4(R/8) + R%4 hold head y + 4hf + 2(r%2) + 8(r/2), so a lane has
+// accumulators 2hf and 2hf+1 (heads y + 2i + 8m) for m = 0..7 in registers
+// 2m and 2m+1.
+__device__ __forceinline__ int head_of_row(int R, int y) {
+  const int r = 4 * (R >> 3) + (R & 3);
+  return y + 4 * ((R >> 2) & 1) + 2 * (r & 1) + 8 * (r >> 1);
+}
+
+__device__ __forceinline__ int n_valid_w(const WideParams& p, int t) {
+  if (t >= p.S) return 0;
+  if (!p.causal) return p.T;
+  const int n = (t + 1) / p.ratio;
+  return n < p.T ? n : p.T;
+}
+
+__device__ __forceinline__ uint32_t order_key16(uint32_t sc) {
+  uint32_t u = (sc ^ ((sc & 0x8000u) ? 0xffffu : 0x8000u)) & 0xffffu;
+  if ((sc & 0x7fffu) > 0x7f80u) u = 0xffffu;  // NaN ranks above everything
+  return u;
+}
+
+// Full wave over a 256-bin histogram (bins ascending in key): the bin b with
+// count(bins > b) < need <= count(bins >= b); gt = count(bins > b).
+__device__ __forceinline__ int find_bin64(const uint32_t* hist, int lane, uint32_t need, uint32_t& gt) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(hist + 4 * lane);
+  const uint32_t local = v[0] + v[1] + v[2] + v[3];
+  uint32_t incl = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl(incl, (lane + off) & 63, 64);
+    if (lane + off < 64) incl += o;
+  }
+  uint32_t cum = incl - local;
+  int fb = -1;
+  uint32_t fgt = 0;
+#pragma unroll
+  for (int i = 3; i >= 0; --i) {
+    const uint32_t nc = cum + v[i];
+    if (cum < need && nc >= need) {
+      fb = 4 * lane + i;
+      fgt = cum;
+    }
+    cum = nc;
+  }
+  const uint64_t m = __ballot(fb >= 0);
+  const int src = m ? (int)__builtin_ctzll(m) : 0;
+  gt = __shfl(fgt, src, 64);
+  return __shfl(fb, src, 64);
+}
+
+__global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint16_t* keys = reinterpret_cast<uint16_t*>(smem);                                   // [kTok][tpad]
+  u32x4* ring = reinterpret_cast<u32x4*>(smem + (size_t)kTok * p.tpad * 2);           // [kRingW][512]
+  float* xbuf = reinterpret_cast<float*>(ring + kRingW * 512);                         // [2][kTok][32]
+  uint32_t* hist = reinterpret_cast<uint32_t*>(xbuf + 2 * kTok * kTileC);             // [kTok][2][256]
+  int32_t* sel = reinterpret_cast<int32_t*>(hist + kTok * 512);                       // [kTok][4]
+  uint32_t* sortbuf = reinterpret_cast<uint32_t*>(ring);  // [kTok][psort], after the scores
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wi = tid >> 6;
+  const int tl = wi >> 1;  // token slot
+  const int y = wi & 1;    // head parity
+  const int hf = lane >> 5;
+  const int col = lane & 31;
+  // Longest causal rows first: the last token groups of every batch start first.
+  const int b = blockIdx.x % p.B;
+  const int grp = p.groups - 1 - (int)(blockIdx.x / p.B);
+  const int t0 = grp * kTok;
+  const int t = t0 + tl;
+  const bool tok_ok = t < p.S;
+  const int nv = n_valid_w(p, t);
+  const int nv_max = n_valid_w(p, min(t0 + kTok - 1, p.S - 1));
+  const int ntiles = (nv_max + kTileC - 1) / kTileC;
+  const int64_t row_bt = (int64_t)b * p.S + (tok_ok ? t : 0);
+  uint16_t* mykeys = keys + tl * p.tpad;
+
+  // Q fragments (A operand): row col -> head hq; channels 16ks + 8hf .. +7, RoPE'd on the fly.
+  const int hq = head_of_row(col, y);
+  bf16x8 qa[8];
+  {
+    const uint16_t* qrow = p.q + (row_bt * kWH + hq) * kWD + 8 * hf;
+    const int half_rd = p.rd >> 1;
+    const int rbase = kWD - p.rd;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      u32x4 v = tok_ok ? *reinterpret_cast<const u32x4*>(qrow + 16 * ks) : u32x4{0u, 0u, 0u, 0u};
+      if (p.freqs != nullptr && tok_ok) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int d0 = 16 * ks + 8 * hf + 2 * w;
+          if (d0 >= rbase) {
+            const int pj = (d0 - rbase) >> 1;
+            const int64_t n = (row_bt * kWH + hq) * half_rd + pj;
+            const float c = p.freqs[((int64_t)t * half_rd + pj) * 2];
+            const float d = p.freqs[((int64_t)t * half_rd + pj) * 2 + 1];
+            float re, im;
+            rope_pair(bf_lo(v[w]), bf_hi(v[w]), c, d, p.rope_mode, n, re, im);
+            v[w] = pack_bf2(re, im);
+          }
+        }
+      }
+      qa[ks] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  // Head weights of the lane's 16 heads as dot2 operands: wlo[m] = (w(h0), 0),
+  // whi[m] = (0, w(h0 + 2)) with h0 = y + 4hf + 8m.
+  uint32_t wlo[8], whi[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int h0 = y + 4 * hf + 8 * m;
+    uint32_t w0 = 0, w1 = 0;
+    if (tok_ok) {
+      w0 = f2bf(bf2f(p.wl[row_bt * kWH + h0]) * p.wscale);
+      w1 = f2bf(bf2f(p.wl[row_bt * kWH + h0 + 2]) * p.wscale);
+    }
+    wlo[m] = w0;
+    whi[m] = w1 << 16;
+  }
+  // bf16 pairs (1, 0) and (0, 1) in SGPRs: as literals the compiler would encode
+  // (1, 0) as the inline constant 1.0, which v_dot2c reads as the fp32 pattern.
+  uint32_t one_lo_bits = 0x00003f80u, one_hi_bits = 0x3f800000u;
+  asm volatile("" : "+s"(one_lo_bits), "+s"(one_hi_bits));
+  const bf16v2 one_lo = __builtin_bit_cast(bf16v2, one_lo_bits);
+  const bf16v2 one_hi = __builtin_bit_cast(bf16v2, one_hi_bits);
+
+  // Tile copies: wave wi moves unit wi (rows 4wi .. 4wi+3 of the tile).
+  const i32x4 rsrc = make_rsrc(p.kv + (int64_t)b * p.kvbs, (uint32_t)p.T * (uint32_t)(kWD * 2));
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4*)ring;
+  const int wis = __builtin_amdgcn_readfirstlane(wi);
+  const int urow = 4 * wis + (lane >> 4);
+  const uint32_t uoff = 16u * (uint32_t)((lane & 15) ^ (urow & 15));
+  const uint32_t ulds = ring_lds + 1024u * (uint32_t)wis;
+  auto issue = [&](int n) {
+    lds_dma16(rsrc, (uint32_t)(kTileC * n + urow) * (uint32_t)(kWD * 2) + uoff,
+              ulds + 8192u * (uint32_t)(n % kRingW));
+  };
+#pragma unroll
+  for (int j = 0; j < kRingW - 1; ++j)
+    if (j < ntiles) issue(j);
+  // Consume the compiler-tracked loads here (their vmcnt(0) also covers the copies).
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) asm volatile("" ::"v"(qa[ks]));
+#pragma unroll
+  for (int m = 0; m < 8; ++m) asm volatile("" ::"v"(wlo[m]), "v"(whi[m]));
+
+  const bool dump = p.scores != nullptr;
+  float t0val = 0.f;  // even-head total of the previous tile (y == 0 waves, upper lanes)
+  // Keys of tile n-1: even + odd totals -> bf16 -> order key (or raw bits when dumping).
+  auto finalize = [&](int n) {
+    if (y == 0 && hf == 1) {
+      const float tot = t0val + xbuf[((n & 1) * kTok + tl) * kTileC + col];
+      uint32_t sc = f2bf(tot);
+      if (p.causal) sc = f2bf(bf2f(sc) + 0.0f);  // the reference adds the 0 / -inf mask
+      const int c = kTileC * n + col;
+      if (c < nv) mykeys[c] = (uint16_t)(dump ? sc : order_key16(sc));
+    }
+  };
+
+  for (int n = 0; n < ntiles; ++n) {
+    if (n + 2 < ntiles) wait_vmcnt<2>();
+    else if (n + 1 < ntiles) wait_vmcnt<1>();
+    else wait_vmcnt<0>();
+    __syncthreads();  // tile n is in LDS; tile n-1's buffer and odd totals are consumed/visible
+    if (n > 0) finalize(n - 1);
+    if (n + kRingW - 1 < ntiles) issue(n + kRingW - 1);
+
+    const u32x4* kt = ring + (n % kRingW) * 512;
+    f32x16 s = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8 bk = __builtin_bit_cast(bf16x8, kt[swz(col, 2 * ks + hf)]);
+      s = mfma32x32x16(qa[ks], bk, s);
+    }
+    float acc_a = 0.f, acc_b = 0.f;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      s16v2 pk = __builtin_bit_cast(s16v2, pack_bf2(s[2 * m], s[2 * m + 1]));
+      pk = __builtin_elementwise_max(pk, (s16v2){0, 0});  // relu on the bf16 bit patterns
+      const bf16v2 pv = __builtin_bit_cast(bf16v2, pk);
+      const float p0 = __builtin_amdgcn_fdot2_f32_bf16(pv, __builtin_bit_cast(bf16v2, wlo[m]), 0.0f, false);
+      const float p1 = __builtin_amdgcn_fdot2_f32_bf16(pv, __builtin_bit_cast(bf16v2, whi[m]), 0.0f, false);
+      const bf16v2 pp = __builtin_bit_cast(bf16v2, pack_bf2(p0, p1));
+      acc_a = __builtin_amdgcn_fdot2_f32_bf16(pp, one_lo, acc_a, false);
+      acc_b = __builtin_amdgcn_fdot2_f32_bf16(pp, one_hi, acc_b, false);
+    }
+    // Lower lanes hold accumulators 0, 1; upper lanes 2, 3 of the same candidate.
+    const float a01 = acc_a + acc_b;
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a01), __float_as_uint(a01), false, false);
+    const float ty = (__uint_as_float(sw[0]) + acc_a) + acc_b;  // valid in the upper lanes
+    if (y == 1) {
+      if (hf == 1) xbuf[((n & 1) * kTok + tl) * kTileC + col] = ty;
+    } else {
+      t0val = ty;
+    }
+  }
+  __syncthreads();
+  if (ntiles > 0) finalize(ntiles - 1);
+  __syncthreads();
+
+  const int tt = y * 64 + lane;  // thread of the token (0..127)
+  if (dump) {
+    if (tok_ok) {
+      uint16_t* dst = p.scores + row_bt * p.T;
+      for (int c = tt; c < p.T; c += 128) dst[c] = c < nv ? mykeys[c] : (uint16_t)0xff80u;
+    }
+    return;
+  }
+
+  // ---------------- top-K of the token: radix select, compaction, bitonic sort
+  const int K = p.K;
+  const bool selecting = nv > K;
+  uint32_t* h1 = hist + tl * 512;
+  uint32_t* h2 = h1 + 256;
+  for (int i = tt; i < 512; i += 128) h1[i] = 0u;
+  __syncthreads();
+  if (selecting)
+    for (int c = tt; c < nv; c += 128) atomicAdd(&h1[mykeys[c] >> 8], 1u);
+  __syncthreads();
+  if (selecting && y == 0) {
+    uint32_t gt;
+    const int b1 = find_bin64(h1, lane, (uint32_t)K, gt);
+    if (lane == 0) {
+      sel[tl * 4 + 0] = b1;
+      sel[tl * 4 + 1] = (int32_t)gt;
+    }
+  }
+  __syncthreads();
+  const int b1 = sel[tl * 4 + 0];
+  if (selecting)
+    for (int c = tt; c < nv; c += 128) {
+      const uint32_t u = mykeys[c];
+      if ((int)(u >> 8) == b1) atomicAdd(&h2[u & 255u], 1u);
+    }
+  __syncthreads();
+  if (selecting && y == 0) {
+    uint32_t gt;
+    const uint32_t above = (uint32_t)sel[tl * 4 + 1];
+    const int b0 = find_bin64(h2, lane, (uint32_t)K - above, gt);
+    if (lane == 0) {
+      sel[tl * 4 + 2] = b0;
+      sel[tl * 4 + 3] = (int32_t)(above + gt);
+    }
+  }
+  __syncthreads();
+  uint32_t* sb = sortbuf + tl * p.psort;
+  const int count = selecting ? K : nv;  // picks that are real candidates
+  if (selecting) {
+    if (y == 0) {
+      const uint32_t kth = ((uint32_t)b1 << 8) | (uint32_t)sel[tl * 4 + 2];
+      const uint32_t n_gt = (uint32_t)sel[tl * 4 + 3];
+      const uint32_t need_eq = (uint32_t)K - n_gt;
+      uint32_t run_gt = 0, run_eq = 0;
+      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+      for (int c0 = 0; c0 < nv; c0 += 64) {
+        const int c = c0 + lane;
+        const uint32_t u = c < nv ? (uint32_t)mykeys[c] : 0u;
+        const bool g = c < nv && u > kth;
+        const bool e = c < nv && u == kth;
+        const uint64_t mg = __ballot(g), me = __ballot(e);
+        const uint32_t comp = (u << 16) | (0xffffu - (uint32_t)c);
+        if (g) sb[run_gt + __builtin_popcountll(mg & below)] = comp;
+        if (e) {
+          const uint32_t r = run_eq + __builtin_popcountll(me & below);
+          if (r < need_eq) sb[n_gt + r] = comp;
+        }
+        run_gt += __builtin_popcountll(mg);
+        run_eq += __builtin_popcountll(me);
+      }
+    }
+  } else {
+    for (int c = tt; c < nv; c += 128) sb[c] = ((uint32_t)mykeys[c] << 16) | (0xffffu - (uint32_t)c);
+  }
+  for (int j = count + tt; j < p.psort; j += 128) sb[j] = 0u;  // sorts last
+  __syncthreads();
+  // Bitonic sort, descending, of psort entries per token (128 threads each).
+  for (int size = 2; size <= p.psort; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tt; i < (p.psort >> 1); i += 128) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint32_t a = sb[lo], c = sb[hi];
+        if ((a < c) == desc) {
+          sb[lo] = c;
+          sb[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (tok_ok) {
+    int64_t* dst = p.out + row_bt * K;
+    for (int j = tt; j < K; j += 128) {
+      const uint32_t comp = sb[j];
+      const int64_t c = (int64_t)(0xffffu - (comp & 0xffffu));
+      dst[j] = (j < count) ? c + p.offset : (int64_t)-1;
+    }
+  }
+}
+
+}  // namespace
+
+// Called by the indexer entry points for h == 64, d == 128 (checks common to both
+// configurations are done by the caller).
+int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batch_stride,
+                            const void* wl, float w_scale, const void* freqs_cis,
+                            int32_t rope_mode, int64_t* out, uint16_t* scores, int64_t b,
+                            int64_t s, int64_t rd, int64_t n_cand, int64_t k_out,
+                            int64_t ratio, int32_t causal, int64_t offset, hipStream_t stream) {
+  // The head-sum order reproduced here is torch's for a candidate count that is a
+  // multiple of 4 (its reduction kernel vectorizes the output by 4 then).
+  if (n_cand > kMaxT || (n_cand % 4) != 0) return DSA_ERR_UNSUPPORTED;
+  if (k_out > kMaxK) return DSA_ERR_UNSUPPORTED;
+  WideParams p;
+  p.q = (const uint16_t*)q;
+  p.kv = (const uint16_t*)kv_cache;
+  p.kvbs = kv_batch_stride;
+  p.wl = (const uint16_t*)wl;
+  p.wscale = w_scale;
+  p.freqs = (const float*)freqs_cis;
+  p.rope_mode = rope_mode;
+  p.out = out;
+  p.scores = scores;
+  p.B = (int32_t)b;
+  p.S = (int32_t)s;
+  p.rd = (int32_t)rd;
+  p.T = (int32_t)n_cand;
+  p.K = (int32_t)k_out;
+  p.ratio = (int32_t)(ratio > (1 << 30) ? (1 << 30) : ratio);
+  p.causal = causal ? 1 : 0;
+  p.offset = offset;
+  p.groups = (int32_t)((s + kTok - 1) / kTok);
+  p.tpad = (int32_t)((n_cand + kTileC - 1) / kTileC * kTileC);
+  int ps = 1;
+  while (ps < k_out) ps <<= 1;
+  p.psort = ps;
+  const size_t smem = (size_t)kTok * p.tpad * 2 + (size_t)kRingW * 8192 + 2 * kTok * kTileC * 4 +
+                      kTok * 512 * 4 + kTok * 4 * 4;
+  if (smem > 160 * 1024) return DSA_ERR_UNSUPPORTED;
+  if (hipFuncSetAttribute((const void*)ix_wide_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)smem) != hipSuccess)
+    return DSA_ERR_LAUNCH;
+  const int64_t blocks = b * p.groups;
+  if (blocks > INT32_MAX) return DSA_ERR_SHAPE;
+  hipLaunchKernelGGL(ix_wide_kernel, dim3((unsigned)blocks), dim3(512), smem, stream, p);
+  return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+}

@@ -182,3 +182,28 @@ def get_init_inputs(device: str = "cuda"):
     kv_cache = torch.randn(a.max_batch_size, a.max_seq_len // compress_ratio, a.index_head_dim,
                            dtype=torch.bfloat16).to(device)
     return [a, freqs_cis, kv_cache, compress_ratio]
+
+
+# ---------------------------------------------------------------- the DSA layer indexer
+def c5_args() -> ModelArgs:
+    """configs[4] indexer: 64 heads x 128 from qr[1,8192,1536] and x[1,8192,7168], top-2048.
+    rope_head_dim is not given by the config; the ModelArgs default (64) is used."""
+    return ModelArgs(max_batch_size=1, max_seq_len=8192, dim=7168, index_n_heads=64,
+                     index_head_dim=128, index_topk=2048, q_lora_rank=1536, rope_head_dim=64)
+
+
+def get_c5_init_inputs(device: str = "cuda", compress_ratio: int = 1):
+    """Constructor inputs for configs[4]: kv_cache [1, 8192, 128] bf16 ~N(0,1), ratio 1."""
+    a = c5_args()
+    freqs_cis = precompute_freqs_cis(a.rope_head_dim, a.max_seq_len, 10000.0, device)
+    kv_cache = torch.randn(a.max_batch_size, a.max_seq_len // compress_ratio, a.index_head_dim,
+                           dtype=torch.bfloat16).to(device)
+    return [a, freqs_cis, kv_cache, compress_ratio]
+
+
+def get_c5_inputs(device: str = "cuda"):
+    """Forward inputs for configs[4]: x [1, 8192, 7168], qr [1, 8192, 1536] bf16 ~N(0,1)."""
+    a = c5_args()
+    x = torch.randn(1, a.max_seq_len, a.dim, dtype=torch.bfloat16).to(device)
+    qr = torch.randn(1, a.max_seq_len, a.q_lora_rank, dtype=torch.bfloat16).to(device)
+    return [x, qr, 0, 0]

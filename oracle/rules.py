@@ -14,9 +14,11 @@ HIP kernel against the same rules.
                   'torch_rocm' torch-ROCm's broadcast multiply: unroll slot (n//128)%4 < 3
                                re = fma(a, c, -(b*d)), im = fma(b, c, a*d); slot 3
                                re = fma(-b, d, a*c),  im = (a*d) + (b*c)
-  head_sum        fp32 sum over 16 heads (task2_v0_ref.py:134): 'rocm' = four running
-                  accumulators over heads j, j+4, j+8, j+12, combined ((a0+a1)+a2)+a3;
-                  'seq' = one accumulator in head order
+  head_sum        fp32 sum over the heads (task2_v0_ref.py:134): 'rocm' = four running
+                  accumulators over heads j, j+4, j+8, j+12, combined ((a0+a1)+a2)+a3
+                  (16 heads); 'rocm_split2' = that over the even and over the odd heads,
+                  then even + odd (64 heads, candidate count % 4 == 0); 'seq' = one
+                  accumulator in head order
   score_chain     bf16(head_sum(bf16(relu(bf16(S)) * w)))
   topk_order      indices of the k largest bf16 values, value descending then index
                   ascending (a stable order); -1/offset fill of task2_v0_ref.py:139-143
@@ -85,8 +87,22 @@ def rope_bf16(q_bits, freqs, rd: int, mode: str, flat_offset: int = 0) -> np.nda
 
 
 def head_sum(v, order: str = "rocm") -> np.ndarray:
-    """fp32 sum over the last axis (16 heads) in torch's accumulation order."""
+    """fp32 sum over the last axis (the heads) in torch's accumulation order.
+
+    'rocm'        one thread, four accumulators over heads j, j+4, j+8, ... combined
+                  ((a0+a1)+a2)+a3 (torch-ROCm's reduction of a short middle dimension,
+                  e.g. 16 heads);
+    'rocm_split2' two threads over the even and the odd heads, each as 'rocm' over its
+                  heads (accumulator i of thread y: heads y+2i+8m), then even + odd
+                  (torch-ROCm for 64 heads with a candidate count divisible by 4);
+    'seq'         one accumulator in head order."""
     v = np.asarray(v, np.float32)
+    if order == "rocm_split2":
+        if v.shape[-1] % 8:
+            raise ValueError(order)
+        even = head_sum(v[..., 0::2], "rocm")
+        odd = head_sum(v[..., 1::2], "rocm")
+        return (even + odd).astype(np.float32)
     if order == "seq":
         acc = np.zeros(v.shape[:-1], np.float32)
         for i in range(v.shape[-1]):
@@ -104,7 +120,8 @@ def head_sum(v, order: str = "rocm") -> np.ndarray:
 
 
 def score_chain(s_bits, w_bits, order: str = "rocm") -> np.ndarray:
-    """bf16 score bits [..., T] from S bits [..., H, T] and w bits [..., H]."""
+    """bf16 score bits [..., T] from S bits [..., H, T] and w bits [..., H] (head-sum order
+    as in head_sum)."""
     s = bf16_to_f32(s_bits)
     s = np.maximum(s, np.float32(0))
     w = bf16_to_f32(w_bits)[..., None]

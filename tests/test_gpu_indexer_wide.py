@@ -1,0 +1,146 @@
+"""Task2 wide configuration (configs[4] indexer: 64 heads x 128, top-2048) on the MI355X.
+
+1. torch-ROCm's 64-head sum against rules.head_sum('rocm_split2') (pins the order).
+2. The bf16 index scores of the wide kernel against the oracle run on the same GPU.
+3. int64 indices through the drop-in Model against the oracle (torch.equal, ties
+   included), from small shapes to the full configs[4] size.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import bits_of
+from ascendc_kernel_amd import _native
+from ascendc_kernel_amd import task2_indexer as t2
+from oracle import indexer as oix
+from oracle import rules
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _wide_bits(shape, g):
+    sgn = torch.randint(0, 2, shape, generator=g, dtype=torch.int32)
+    ex = torch.randint(115, 139, shape, generator=g, dtype=torch.int32)
+    mn = torch.randint(0, 128, shape, generator=g, dtype=torch.int32)
+    return ((sgn << 15) | (ex << 7) | mn).to(torch.int16).view(torch.bfloat16)
+
+
+def test_torch_head_sum_rule_64(gpu):
+    """x[1, 512, 64, 1024].sum(dim=2): two threads (even / odd heads), four accumulators each."""
+    g = torch.Generator().manual_seed(11)
+    x = _wide_bits((1, 512, 64, 1024), g)
+    _say("rule head-sum 64")
+    got = bits_of(x.to(gpu).sum(dim=2))
+    xs = rules.bf16_to_f32(bits_of(x[:, :64]))
+    want = rules.bf16_round(rules.head_sum(np.moveaxis(xs, 2, -1), "rocm_split2"))
+    assert np.array_equal(got[:, :64], want), int((got[:, :64] != want).sum())
+    other = rules.bf16_round(rules.head_sum(np.moveaxis(xs, 2, -1), "rocm"))
+    assert not np.array_equal(other, want)  # the planted data tells the two orders apart
+
+
+def _args(seqlen, topk, rd=64):
+    return oix.IndexerArgs(max_batch_size=1, max_seq_len=seqlen, dim=7168, q_lora_rank=1536,
+                           rope_head_dim=rd, index_n_heads=64, index_head_dim=128, index_topk=topk)
+
+
+def _pair(args, seed, kv_rows, ratio, device, wstd=None):
+    torch.manual_seed(seed)
+    fr = oix.precompute_freqs_cis(args.rope_head_dim, args.max_seq_len, device=device)
+    kv = torch.randn(args.max_batch_size, kv_rows, args.index_head_dim, dtype=torch.bfloat16).to(device)
+    torch.manual_seed(seed + 1)
+    m = t2.Model(args, fr, kv, ratio).to(device)
+    if wstd is not None:
+        g = torch.Generator().manual_seed(seed + 2)
+        with torch.no_grad():
+            for p in (m.wq_b.weight, m.weights_proj.weight):
+                p.copy_((torch.randn(p.shape, generator=g) * wstd).to(torch.bfloat16))
+    r = oix.IndexerRef(args, fr, kv, ratio).to(device)
+    r.wq_b.weight.data.copy_(m.wq_b.weight.data)
+    r.weights_proj.weight.data.copy_(m.weights_proj.weight.data)
+    return m, r
+
+
+def _check_equal(got, want, name):
+    eq = torch.equal(got, want)
+    if not eq:
+        rows = (got != want).any(dim=-1)
+        r0 = int(torch.nonzero(rows.view(-1))[0])
+        _say(f"[{name}] mismatching rows {int(rows.sum())} of {rows.numel()}; first {r0}:",
+             got.view(-1, got.shape[-1])[r0, :12].tolist(), want.view(-1, want.shape[-1])[r0, :12].tolist())
+    assert eq, name
+
+
+@pytest.mark.parametrize("seqlen,start_pos", [(512, 0), (96, 0), (64, 128)])
+def test_wide_score_stage_matches_torch(gpu, seqlen, start_pos):
+    args = _args(start_pos + seqlen, 2048)
+    m, r = _pair(args, 31, start_pos + seqlen, 1, gpu, wstd=0.02)
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(1, seqlen, 7168, generator=g).to(torch.bfloat16).to(gpu)
+    qr = torch.randn(1, seqlen, 1536, generator=g).to(torch.bfloat16).to(gpu)
+    end = start_pos + seqlen
+    _say("wide score stage", seqlen, start_pos)
+    want = oix.index_scores(r.wq_b.weight, r.weights_proj.weight, r.kv_cache, r.freqs_cis, x, qr,
+                            start_pos, 64, 128, 64, 1)
+    q = torch.nn.functional.linear(qr, m.wq_b.weight).unflatten(-1, (64, 128)).contiguous()
+    wl = torch.nn.functional.linear(x, m.weights_proj.weight)
+    got = _native.indexer_scores(q, m.kv_cache, wl, 128 ** -0.5 * 64 ** -0.5, m.freqs_cis[start_pos:end],
+                                 64, end, 1, start_pos == 0)
+    gb, wb = bits_of(got), bits_of(want)
+    ne = gb != wb
+    if ne.any():
+        i = np.argwhere(ne)[:6]
+        _say("first mismatches:", [(tuple(int(v) for v in ii), hex(gb[tuple(ii)]), hex(wb[tuple(ii)])) for ii in i],
+             "fraction", float(ne.mean()))
+    assert not ne.any(), int(ne.sum())
+
+
+WIDE = [
+    # seqlen, start_pos, offset, topk, ratio
+    (512, 0, 0, 128, 1),
+    (1024, 0, 5, 2048, 1),
+    (700, 0, 0, 300, 1),
+    (64, 128, 7, 64, 1),
+    (256, 0, 0, 96, 2),
+]
+
+
+@pytest.mark.parametrize("case", WIDE)
+def test_wide_shapes_and_modes(gpu, case):
+    seqlen, start_pos, offset, topk, ratio = case
+    end = start_pos + seqlen
+    args = _args(end, topk)
+    m, r = _pair(args, 200 + seqlen, end // ratio, ratio, gpu, wstd=0.02)
+    g = torch.Generator().manual_seed(seqlen + 1)
+    x = torch.randn(1, seqlen, 7168, generator=g).to(torch.bfloat16).to(gpu)
+    qr = torch.randn(1, seqlen, 1536, generator=g).to(torch.bfloat16).to(gpu)
+    _say("wide case", case)
+    _check_equal(m(x, qr, start_pos, offset), r(x, qr, start_pos, offset), f"wide{case}")
+
+
+def test_full_shape_c5_indexer(gpu):
+    """configs[4] indexer: x[1,8192,7168], qr[1,8192,1536], kv_cache[1,8192,128], W ~ N(0, 0.02),
+    causal, top-2048, ratio 1, rope_head_dim 64."""
+    torch.manual_seed(42)
+    init = t2.get_c5_init_inputs(device=gpu)
+    m = t2.Model(*init).to(gpu)
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        for p in (m.wq_b.weight, m.weights_proj.weight):
+            p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(torch.bfloat16))
+    r = oix.IndexerRef(*init).to(gpu)
+    r.wq_b.weight.data.copy_(m.wq_b.weight.data)
+    r.weights_proj.weight.data.copy_(m.weights_proj.weight.data)
+    torch.manual_seed(43)
+    x, qr, sp, off = t2.get_c5_inputs(device=gpu)
+    _say("case c5 indexer full shape")
+    with torch.no_grad():
+        got = m(x, qr, sp, off)
+        torch.cuda.synchronize()
+        _say("case c5 oracle")
+        want = r(x, qr, sp, off)
+        torch.cuda.synchronize()
+    _check_equal(got, want, "c5-indexer")

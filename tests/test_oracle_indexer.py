@@ -168,3 +168,18 @@ def test_topk_torch_rule_network_and_known_orders():
     # k > 32 is the stable order
     row = np.array([[0x3f80] * 40 + [0x4000] * 10], np.uint16)
     assert rules.topk_torch(row, 40)[0].tolist() == list(range(40, 50)) + list(range(30))
+
+
+def test_head_sum_split2_rule():
+    """'rocm_split2' = even-head and odd-head 'rocm' sums, then added; equal to every other
+    order when the sums are exact, different on planted wide-exponent data."""
+    rng = np.random.default_rng(5)
+    v = rng.integers(-50, 50, size=(40, 64)).astype(np.float32)
+    exact = v.sum(axis=-1, dtype=np.float64).astype(np.float32)
+    for order in ("seq", "rocm", "rocm_split2"):
+        assert np.array_equal(rules.head_sum(v, order), exact)
+    w = (rng.standard_normal((4000, 64)) * np.exp2(rng.integers(-12, 12, (4000, 64)))).astype(np.float32)
+    s2 = rules.head_sum(w, "rocm_split2")
+    even, odd = rules.head_sum(w[:, 0::2], "rocm"), rules.head_sum(w[:, 1::2], "rocm")
+    assert np.array_equal(s2, (even + odd).astype(np.float32))
+    assert not np.array_equal(s2, rules.head_sum(w, "rocm"))
