@@ -27,6 +27,7 @@ EXPORTS = (
     "dsa_abi_version",
     "dsa_strerror",
     "dsa_sparse_attn_fwd",
+    "dsa_sparse_mla_fwd",
     "dsa_indexer_rope",
     "dsa_indexer_score_topk",
     "dsa_indexer_scores",
@@ -69,6 +70,11 @@ def load() -> ctypes.CDLL:
         _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
         ctypes.c_float, ctypes.c_int32, _c_vp]
+    lib.dsa_sparse_mla_fwd.restype = ctypes.c_int
+    lib.dsa_sparse_mla_fwd.argtypes = [
+        _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        ctypes.c_float, _c_vp]
     lib.dsa_indexer_rope.restype = ctypes.c_int
     lib.dsa_indexer_rope.argtypes = [
         _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32, _c_vp]
@@ -136,6 +142,36 @@ def sparse_attn_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
         q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), out.data_ptr(),
         b, m, h, d, kv.shape[1], idx.shape[2], float(softmax_scale), int(variant), _stream(q))
     _check("dsa_sparse_attn_fwd", rc)
+    return out
+
+
+def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
+                   attn_sink: torch.Tensor, softmax_scale: float, v_dim: int) -> torch.Tensor:
+    """Sparse MLA on the GPU: q [b,m,h,d_qk], kv [b,n_kv,>=d_qk]; keys are kv[..., :d_qk],
+    values kv[..., :v_dim]; returns bf16 [b,m,h,v_dim]."""
+    lib = load()
+    if q.dim() != 4 or kv.dim() != 3 or topk_idxs.dim() != 3:
+        raise ValueError("expected q [b,m,h,d_qk], kv [b,n_kv,kv_dim], topk_idxs [b,m,topk]")
+    b, m, h, dqk = q.shape
+    if kv.shape[0] != b or kv.shape[2] < dqk or tuple(topk_idxs.shape[:2]) != (b, m):
+        raise ValueError(f"inconsistent shapes q{tuple(q.shape)} kv{tuple(kv.shape)} "
+                         f"topk_idxs{tuple(topk_idxs.shape)}")
+    if q.dtype != torch.bfloat16 or kv.dtype != torch.bfloat16:
+        raise TypeError("q and kv must be bfloat16")
+    if topk_idxs.dtype not in (torch.int32, torch.int64):
+        raise TypeError("topk_idxs must be int32 or int64")
+    if attn_sink.numel() != h:
+        raise ValueError(f"attn_sink has {attn_sink.numel()} entries, expected {h}")
+    dev = _require_gpu(q, kv, topk_idxs)
+    q = q.contiguous()
+    kv = kv.contiguous()
+    idx = topk_idxs.to(torch.int32).contiguous() if topk_idxs.dtype != torch.int32 else topk_idxs.contiguous()
+    sink = attn_sink.detach().to(device=dev, dtype=torch.float32).contiguous()
+    out = torch.empty(b, m, h, v_dim, dtype=torch.bfloat16, device=dev)
+    rc = lib.dsa_sparse_mla_fwd(
+        q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), out.data_ptr(),
+        b, m, h, dqk, v_dim, kv.shape[2], kv.shape[1], idx.shape[2], float(softmax_scale), _stream(q))
+    _check("dsa_sparse_mla_fwd", rc)
     return out
 
 

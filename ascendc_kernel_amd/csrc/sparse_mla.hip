@@ -1,0 +1,368 @@
+// Sparse MLA forward: the attention of the DSA layer. It is Task1's
+// sparse attention (reference/task1_v0_ref.py:5-24: gather, fp32 scores with the
+// sink in the softmax denominator, bf16 output) with one latent kv row serving as
+// the key (its first d_qk = 576 channels) and as the value (its first d_v = 512
+// channels): out[b,m,h,:] = sum_t softmax_t(scale * q . kv_t[:576]) kv_t[:512].
+//
+// One workgroup per token, one wave per 16 heads (8 waves for 128 heads). Per
+// wave, Q^T (576 x 16 heads, 72 VGPRs) and O^T (512 x 16, fp32, 128 registers)
+// stay in registers. Slots go in blocks of 32: the 32 selected rows (1152 B each)
+// are copied by buffer_load ... lds into a ring of 4 LDS buffers, each row padded
+// to 73 chunks of 16 B so that one chunk read across 16 rows, and the transposed
+// reads of V, hit distinct banks. Per block and wave (mfma 16x16x32, lane l:
+// head l%16, key / channel group g = l/16):
+//   S^T[2 x 16 keys x 16 heads] = K . Q^T                  (2 x 18 mfma)
+//   online softmax over the 32 keys of a head (held by the 4 lane groups, reduced
+//   with permlane16/32 swaps), sink as the initial max, log2 domain
+//   O^T[512 x 16] += V^T[512 x 32] . (P_hi + P_lo)^T         (32 x 2 mfma)
+// with the contraction over keys ordered so that each lane's 8 P values are the B
+// operand as they stand (keys 4g..4g+3 and 16+4g..16+4g+3 for lane group g).
+// The two waves of a SIMD overlap one's softmax with the other's products.
+#include "dsa_common.h"
+
+using namespace dsa;
+
+namespace {
+
+constexpr int kDQK = 576;                       // key / query channels
+constexpr int kDV = 512;                        // value channels
+constexpr int kKS = kDQK / 32;                  // 18 k-steps of the score product
+constexpr int kCT = kDV / 16;                   // 32 output tiles of 16 channels
+constexpr int kKB = 32;                         // slots per block
+constexpr int kRowC = kDQK / 8 + 1;             // LDS row: 72 chunks + 1 pad chunk
+constexpr int kBlkPos = kKB * kRowC;            // 2336 chunk positions per block
+constexpr int kUnitsBlk = (kBlkPos + 63) / 64;  // 37 copy units of 64 chunks
+constexpr int kBlkBytes = kUnitsBlk * 1024;     // 37888 B per buffer (copy tail included)
+constexpr int kRingM = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRaise = 8.0f;
+constexpr uint32_t kOob = 0xfffffff0u;          // a copy offset beyond any resource: reads zeros
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+struct MlaParams {
+  const uint16_t* q;     // [B, M, H, 576]
+  const uint16_t* kv;    // [B, NKV, kv_dim] (kv_dim >= 576 channels per row)
+  const int32_t* idx;    // [B, M, TOPK]
+  const float* sink;     // [H]
+  uint16_t* out;         // [B, M, H, 512]
+  int64_t M;
+  int32_t B, H, NKV, TOPK, kv_dim;
+  float scale_log2;
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return i32x4{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a),
+               __builtin_amdgcn_readfirstlane((int32_t)((a >> 32) & 0xffffu)), (int32_t)bytes,
+               0x00020000};
+}
+
+// buffer_load_dwordx4 ... lds (see the gather kernel): lane l copies 16 B at byte
+// offset voff of the resource to LDS address m0 + 16 l; waited with wait_vmcnt.
+__device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t voff, uint32_t m0) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "{m0}"(m0)
+               : "memory");
+}
+
+struct S2 {
+  f32x4 t0, t1;
+};
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sa_mla_kernel(MlaParams p) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint8_t* ring = smem;                                                   // [kRingM][kBlkBytes]
+  int32_t* slot = reinterpret_cast<int32_t*>(smem + kRingM * kBlkBytes);  // [nblk * 32]
+  const int nblk = (p.TOPK + kKB - 1) / kKB;
+  int32_t* nblk_sh = slot + nblk * kKB;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wi = tid >> 6;
+  const int64_t tok = blockIdx.x;
+  const int b = (int)(tok / p.M);
+  const int n = lane & 15;  // head 16wi + n
+  const int g = lane >> 4;  // lane group: k-slice 8g..8g+7, C rows 4g..4g+3
+  const int head = 16 * wi + n;
+  const bool hvalid = head < p.H;
+
+  if (tid == 0) *nblk_sh = 0;
+  __syncthreads();
+  int last = 0;
+  for (int s = tid; s < nblk * kKB; s += 64 * NW) {
+    int v = -1;
+    if (s < p.TOPK) {
+      v = p.idx[tok * p.TOPK + s];
+      if (v >= p.NKV) v = -1;
+    }
+    slot[s] = v;
+    if (v >= 0) last = s / kKB + 1;
+  }
+  if (last > 0) atomicMax(nblk_sh, last);
+
+  // Q^T fragments (B operand): head `head`, channels 32ks + 8g .. +7.
+  bf16x8 qf[kKS];
+  {
+    const uint16_t* qrow = p.q + (tok * p.H + (hvalid ? head : 0)) * kDQK + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < kKS; ++ks)
+      qf[ks] = hvalid ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + 32 * ks))
+                      : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+  }
+  __syncthreads();
+  const int nb = *nblk_sh;
+
+  // Copies: unit u covers chunk positions 64u .. 64u+63 of a block buffer
+  // (position P = row * 73 + chunk). Wave wi moves units wi, wi + NW, ...; every
+  // wave issues kUnitsW copies (surplus ones repeat the last unit: same bytes).
+  constexpr int kUnitsW = (kUnitsBlk + NW - 1) / NW;
+  const int wis = __builtin_amdgcn_readfirstlane(wi);
+  const i32x4 rsrc = make_rsrc(p.kv + (int64_t)b * p.NKV * p.kv_dim,
+                               (uint32_t)p.NKV * (uint32_t)p.kv_dim * 2u);
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;
+  const uint32_t row_bytes = (uint32_t)p.kv_dim * 2u;
+  auto rows_of = [&](int blk, int (&rv)[kUnitsW]) {
+#pragma unroll
+    for (int i = 0; i < kUnitsW; ++i) {
+      int u = wis + NW * i;
+      if (u >= kUnitsBlk) u = kUnitsBlk - 1;
+      const int r = (64 * u + lane) / kRowC;
+      rv[i] = r < kKB ? slot[blk * kKB + r] : -1;
+    }
+  };
+  auto issue = [&](int blk, const int (&rv)[kUnitsW]) {
+    const uint32_t base = ring_lds + (uint32_t)(blk % kRingM) * (uint32_t)kBlkBytes;
+#pragma unroll
+    for (int i = 0; i < kUnitsW; ++i) {
+      int u = wis + NW * i;
+      if (u >= kUnitsBlk) u = kUnitsBlk - 1;
+      const int c = (64 * u + lane) % kRowC;
+      const uint32_t voff =
+          (rv[i] >= 0 && c < kRowC - 1) ? (uint32_t)rv[i] * row_bytes + 16u * (uint32_t)c : kOob;
+      lds_dma16(rsrc, voff, base + 1024u * (uint32_t)u);
+    }
+  };
+
+  f32x4 o[kCT];
+#pragma unroll
+  for (int ct = 0; ct < kCT; ++ct) o[ct] = f32x4{};
+  const float sink_l2 = hvalid ? p.sink[head] * kLog2e : 0.f;
+  const float c2 = p.scale_log2;  // > 0 (checked by the host)
+  float m_run = sink_l2;
+  float l_run = 0.f;
+
+  // S^T of the block in buffer kvl: tile kt has keys 16kt + (lane%16) as A rows,
+  // channels 32ks + 8g; the lane's results are keys 16kt + 4g + r of head n.
+  auto qk = [&](const uint8_t* kvl) {
+    S2 acc = {f32x4{}, f32x4{}};
+    const u32x4* r0 = reinterpret_cast<const u32x4*>(kvl) + n * kRowC + g;
+    const u32x4* r1 = r0 + 16 * kRowC;
+#pragma unroll
+    for (int ks = 0; ks < kKS; ++ks) {
+      acc.t0 = mfma16x16x32(__builtin_bit_cast(bf16x8, r0[4 * ks]), qf[ks], acc.t0);
+      acc.t1 = mfma16x16x32(__builtin_bit_cast(bf16x8, r1[4 * ks]), qf[ks], acc.t1);
+    }
+    return acc;
+  };
+
+  int rv[kUnitsW];
+#pragma unroll
+  for (int j = 0; j < kRingM - 1; ++j) {
+    if (j < nb) {
+      rows_of(j, rv);
+      issue(j, rv);
+    }
+  }
+  if (nb > 0) rows_of(min(kRingM - 1, nb - 1), rv);
+  int vslot = slot[lane & 31];
+#pragma unroll
+  for (int ks = 0; ks < kKS; ++ks) asm volatile("" ::"v"(qf[ks]));
+  asm volatile("" ::"v"(m_run));
+
+  // bf16 pairs (-1, 0), (0, -1) in SGPRs for the dot2 residuals (see the gather kernel).
+  uint32_t neg_lo_bits = 0x0000bf80u, neg_hi_bits = 0xbf800000u;
+  asm volatile("" : "+s"(neg_lo_bits), "+s"(neg_hi_bits));
+  const bf16v2 neg_lo = __builtin_bit_cast(bf16v2, neg_lo_bits);
+  const bf16v2 neg_hi = __builtin_bit_cast(bf16v2, neg_hi_bits);
+
+  static_assert(kRingM == 4, "the waits assume a ring of 4 buffers");
+  uint32_t vm_cur = 0u;
+  auto step = [&](const int kb) {
+    uint32_t vm_next = 0u;
+    if (kb + 1 < nb) {
+      if (kb + 2 < nb) wait_vmcnt<kUnitsW>();
+      else wait_vmcnt<0>();
+      __syncthreads();  // block kb+1 is in LDS; block kb-1's buffer is free
+      if (kb + kRingM - 1 < nb) issue(kb + kRingM - 1, rv);
+      vm_next = (uint32_t)__ballot(vslot >= 0);
+      rows_of(min(kb + kRingM, nb - 1), rv);
+      vslot = slot[min(kb + 2, nb - 1) * kKB + (lane & 31)];
+    }
+    const S2 sc = qk(ring + (kb % kRingM) * kBlkBytes);
+    float sv[8];  // keys 4g + r (r < 4) and 16 + 4g + (r - 4)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sv[r] = sc.t0[r];
+      sv[r + 4] = sc.t1[r];
+    }
+    if (vm_cur != 0xffffffffu) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int key = (r < 4) ? 4 * g + r : 16 + 4 * g + (r - 4);
+        if (!((vm_cur >> key) & 1u)) sv[r] = -INFINITY;
+      }
+    }
+    float bmax = sv[0];
+#pragma unroll
+    for (int r = 1; r < 8; ++r) bmax = fmaxf(bmax, sv[r]);
+    bmax *= c2;
+    {  // max over the 4 lane groups holding the same head
+      const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(bmax), __float_as_uint(bmax), false, false);
+      bmax = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+      const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(bmax), __float_as_uint(bmax), false, false);
+      bmax = fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+    }
+    const bool raise = bmax > m_run + kRaise;
+    if (__ballot(raise) != 0) {
+      const float m_new = raise ? bmax : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int ct = 0; ct < kCT; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[ct][r] *= alpha;
+      m_run = m_new;
+    }
+    float pe[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) pe[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], c2, -m_run));
+#pragma unroll
+    for (int r = 0; r < 8; ++r) l_run += pe[r];
+    u32x4 wh, wl;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float p0 = pe[2 * w], p1 = pe[2 * w + 1];
+      const uint32_t h = pack_bf2(p0, p1);
+      wh[w] = h;
+      const bf16v2 hv = __builtin_bit_cast(bf16v2, h);
+      wl[w] = pack_bf2(__builtin_amdgcn_fdot2_f32_bf16(hv, neg_lo, p0, false),
+                       __builtin_amdgcn_fdot2_f32_bf16(hv, neg_hi, p1, false));
+    }
+    const bf16x8 phi = __builtin_bit_cast(bf16x8, wh);
+    const bf16x8 plo = __builtin_bit_cast(bf16x8, wl);
+    // O^T += V^T . P^T: supplier lane s = lane%16 of group g reads 4 channels
+    // 16ct + 4(s%4) .. +3 of key row 4g + s/4 (first read) and 16 + 4g + s/4
+    // (second); the transposed reads hand channel 16ct + (lane%16) keys
+    // 4g + 0..3 and 16 + 4g + 0..3 to each lane, matching the P operand.
+    const uint16_t* kvh = reinterpret_cast<const uint16_t*>(ring + (kb % kRingM) * kBlkBytes);
+    const uint16_t* row0 = kvh + (4 * g + (n >> 2)) * (kRowC * 8) + 4 * (n & 3);
+    const uint16_t* row1 = row0 + 16 * (kRowC * 8);
+#pragma unroll
+    for (int ct = 0; ct < kCT; ++ct) {
+      const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(row0 + 16 * ct));
+      const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(row1 + 16 * ct));
+      const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      o[ct] = mfma16x16x32(a, plo, o[ct]);
+      o[ct] = mfma16x16x32(a, phi, o[ct]);
+    }
+    vm_cur = vm_next;
+  };
+
+  if (nb > 0) {
+    if (nb >= 3) wait_vmcnt<2 * kUnitsW>();
+    else if (nb == 2) wait_vmcnt<kUnitsW>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    vm_cur = (uint32_t)__ballot(vslot >= 0);
+    vslot = slot[min(1, nb - 1) * kKB + (lane & 31)];
+    for (int kb = 0; kb < nb; ++kb) step(kb);
+  }
+  __syncthreads();  // the ring is reused for the output transpose
+
+  // Z = the sum over the 4 lane groups + exp2(sink - m).
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  const float rz = 1.0f / (l_run + __builtin_amdgcn_exp2f(sink_l2 - m_run));
+  // O^T lane data: head n, channels 16ct + 4g + r. Transpose through LDS: per wave
+  // 16 head rows of 64 chunks (1 KB); chunk q of row n sits at n*64 + (q ^ n).
+  uint8_t* obuf = ring + wi * (16 * 1024);
+#pragma unroll
+  for (int ct = 0; ct < kCT; ++ct) {
+    const uint32_t lo = pack_bf2(o[ct][0] * rz, o[ct][1] * rz);
+    const uint32_t hi = pack_bf2(o[ct][2] * rz, o[ct][3] * rz);
+    const int q = 2 * ct + (g >> 1);
+    *reinterpret_cast<uint2*>(obuf + n * 1024 + (q ^ n) * 16 + 8 * (g & 1)) = uint2{lo, hi};
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  u32x4* dst = reinterpret_cast<u32x4*>(p.out + (tok * p.H + 16 * wi) * kDV);
+  for (int r = 0; r < 16; ++r)
+    if (16 * wi + r < p.H)
+      st_nt(dst + r * 64 + lane, *reinterpret_cast<const u32x4*>(obuf + r * 1024 + (lane ^ r) * 16));
+}
+
+}  // namespace
+
+extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
+                                  const float* attn_sink, void* out, int64_t b, int64_t m,
+                                  int64_t h, int64_t d_qk, int64_t d_v, int64_t kv_dim,
+                                  int64_t n_kv, int64_t topk, float softmax_scale, void* stream) {
+  if (b < 0 || m < 0 || h <= 0 || n_kv < 1 || topk < 1) return DSA_ERR_SHAPE;
+  if (d_qk != kDQK || d_v != kDV || kv_dim < kDQK) return DSA_ERR_UNSUPPORTED;
+  // 4..8 waves of 16 heads (with fewer, a block takes too many copies per wave to
+  // keep two blocks in flight under the 6-bit vmcnt).
+  if (h % 16 != 0 || h < 64 || h > 128 || topk > 2048) return DSA_ERR_UNSUPPORTED;
+  if (!(softmax_scale > 0.f) || !(softmax_scale < INFINITY)) return DSA_ERR_UNSUPPORTED;
+  if (n_kv > (1 << 21) || kv_dim > (1 << 16) || (kv_dim % 8) != 0) return DSA_ERR_UNSUPPORTED;
+  if (b * m > INT32_MAX) return DSA_ERR_SHAPE;
+  if (b == 0 || m == 0) return DSA_OK;
+  if (!q || !kv || !topk_idxs || !attn_sink || !out) return DSA_ERR_NULL;
+  if (!dsa_host::aligned16(q) || !dsa_host::aligned16(kv) || !dsa_host::aligned16(out)) return DSA_ERR_ALIGN;
+  MlaParams p;
+  p.q = (const uint16_t*)q;
+  p.kv = (const uint16_t*)kv;
+  p.idx = topk_idxs;
+  p.sink = attn_sink;
+  p.out = (uint16_t*)out;
+  p.M = m;
+  p.B = (int32_t)b;
+  p.H = (int32_t)h;
+  p.NKV = (int32_t)n_kv;
+  p.TOPK = (int32_t)topk;
+  p.kv_dim = (int32_t)kv_dim;
+  p.scale_log2 = softmax_scale * kLog2e;
+  const int64_t nblk = (topk + kKB - 1) / kKB;
+  const size_t smem = (size_t)kRingM * kBlkBytes + (size_t)nblk * kKB * 4 + 16;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)(b * m));
+  switch (h / 16) {
+#define DSA_MLA_CASE(nw)                                                                          \
+  case nw:                                                                                        \
+    if (hipFuncSetAttribute((const void*)sa_mla_kernel<nw>,                                        \
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)   \
+      return DSA_ERR_LAUNCH;                                                                      \
+    hipLaunchKernelGGL(sa_mla_kernel<nw>, grid, dim3(64 * nw), smem, st, p);                      \
+    break;
+    DSA_MLA_CASE(4)
+    DSA_MLA_CASE(5)
+    DSA_MLA_CASE(6)
+    DSA_MLA_CASE(7)
+    DSA_MLA_CASE(8)
+#undef DSA_MLA_CASE
+    default:
+      return DSA_ERR_UNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+}

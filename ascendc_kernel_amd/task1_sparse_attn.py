@@ -24,10 +24,13 @@ class Model(nn.Module):
     #: kernel choice passed to the C ABI (auto = multiplicity kernel when n_kv <= 32)
     variant: int = _native.DSA_SA_AUTO
 
-    def __init__(self, n_heads: int, head_dim: int):
+    def __init__(self, n_heads: int, head_dim: int, v_dim: int = None):
+        """`v_dim` (not in the reference, default None = head_dim): value width for sparse
+        MLA, where kv rows carry head_dim key channels of which the first v_dim are the value."""
         super().__init__()
         self.n_heads = n_heads
         self.head_dim = head_dim
+        self.v_dim = v_dim
         self.softmax_scale = head_dim ** -0.5
         self.attn_sink = nn.Parameter(torch.zeros(n_heads, dtype=torch.float32))
 
@@ -35,6 +38,9 @@ class Model(nn.Module):
         if q.shape[2] != self.n_heads or q.shape[3] != self.head_dim:
             raise ValueError(f"q {tuple(q.shape)} does not match n_heads={self.n_heads}, "
                              f"head_dim={self.head_dim}")
+        if self.v_dim is not None and self.v_dim != self.head_dim:
+            return _native.sparse_mla_fwd(q, kv, topk_idxs, self.attn_sink, self.softmax_scale,
+                                          self.v_dim)
         return _native.sparse_attn_fwd(q, kv, topk_idxs, self.attn_sink, self.softmax_scale,
                                        self.variant)
 
@@ -76,6 +82,24 @@ def get_gather_inputs(batch_size=4, seq_len=4096, n_kv=8192, topk=512, device="c
     for t0 in range(0, seq_len, step):
         t = torch.arange(t0, min(seq_len, t0 + step), device=device)
         sc = torch.rand(batch_size, len(t), n_kv, generator=g, device=device)
+        sc = sc.masked_fill(cols[None, None, :] > t[None, :, None], -1.0)
+        val, ix = sc.topk(topk, dim=-1)
+        idx[:, t0:t0 + len(t)] = torch.where(val >= 0, ix, torch.full_like(ix, -1)).to(torch.int32)
+    return [q, kv, idx]
+
+
+def get_mla_inputs(seq_len=8192, n_heads_mla=128, d_qk=576, topk=2048, device="cuda", seed=42):
+    """configs[4] sparse-MLA inputs, built on `device`: q [1, m, 128, 576] and the latent
+    kv [1, m, 576] bf16 ~N(0,1); token t selects min(t+1, topk) distinct rows of [0, t]
+    (the causal top-k the indexer hands over), remaining slots -1."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(1, seq_len, n_heads_mla, d_qk, generator=g, device=device).to(torch.bfloat16)
+    kv = torch.randn(1, seq_len, d_qk, generator=g, device=device).to(torch.bfloat16)
+    idx = torch.empty(1, seq_len, topk, dtype=torch.int32, device=device)
+    cols = torch.arange(seq_len, device=device)
+    for t0 in range(0, seq_len, 256):
+        t = torch.arange(t0, min(seq_len, t0 + 256), device=device)
+        sc = torch.rand(1, len(t), seq_len, generator=g, device=device)
         sc = sc.masked_fill(cols[None, None, :] > t[None, :, None], -1.0)
         val, ix = sc.topk(topk, dim=-1)
         idx[:, t0:t0 + len(t)] = torch.where(val >= 0, ix, torch.full_like(ix, -1)).to(torch.int32)

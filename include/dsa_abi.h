@@ -74,6 +74,28 @@ int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
                         float softmax_scale, int32_t variant, void* stream);
 
 /*
+ * Sparse MLA: Task1 with a key wider than the value (the attention of the DSA layer,
+ * configs[4]): one latent kv row is the key (its first d_qk channels) and the value
+ * (its first d_v channels):
+ *   out[b,m,h,:] = sum_t softmax_t(scale * q[b,m,h,:] . kv[b,idx_t,:d_qk] ; sink_h) kv[b,idx_t,:d_v]
+ * Same semantics as sparse_attn_ref (reference/task1_v0_ref.py:5-24, masked slots,
+ * sink in the denominator, fp32 softmax, bf16 output), whose K = V = kv is the case
+ * d_v = d_qk; the reference has no separate value width, this entry point adds it.
+ *
+ *   q          bf16 [b, m, h, d_qk]
+ *   kv         bf16 [b, n_kv, kv_dim]     rows of kv_dim >= d_qk channels
+ *   topk_idxs  int32 [b, m, topk]         negative or >= n_kv = masked slot
+ *   attn_sink  fp32 [h]
+ *   out        bf16 [b, m, h, d_v]
+ * Requirements: d_qk == 576, d_v == 512, h % 16 == 0 with 64 <= h <= 128,
+ * topk <= 2048, n_kv <= 2^21, kv_dim % 8 == 0, softmax_scale > 0; q/kv/out 16-byte aligned.
+ */
+int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
+                       const float* attn_sink, void* out, int64_t b, int64_t m, int64_t h,
+                       int64_t d_qk, int64_t d_v, int64_t kv_dim, int64_t n_kv, int64_t topk,
+                       float softmax_scale, void* stream);
+
+/*
  * Task2 RoPE, in place on the last `rd` channels of every head of q.
  * Replaces apply_rotary_emb(q[..., -rd:], freqs_cis) (reference/task2_v0_ref.py:93-104,131)
  * and the Ascend ix_rope launch (src/indexer_kernel_aiv.asc:19-111; src/task2_indexer.py:1117-1130).
@@ -107,8 +129,11 @@ int dsa_indexer_rope(void* q, const void* freqs_cis, int64_t b, int64_t s, int64
  *   out        int64 [b, s, k_out]
  *   n_cand     number of candidate keys T = end_pos // ratio
  *   causal     1 when start_pos == 0 (mask and -1 fill), else 0
- * Requirements: h == 16, d == 64, rd as for dsa_indexer_rope (when freqs_cis != NULL),
- * 1 <= n_cand <= 2048, 1 <= k_out <= min(n_cand, 256), ratio >= 1.
+ * Requirements: rd as for dsa_indexer_rope (when freqs_cis != NULL), ratio >= 1,
+ * 1 <= k_out <= n_cand, and one of
+ *   h == 16, d == 64:   n_cand <= 2048, k_out <= 256                (configs[2])
+ *   h == 64, d == 128:  n_cand <= 8192, n_cand % 4 == 0, k_out <= 2048 (configs[4]; the
+ *                       head-sum order reproduced is torch's for n_cand % 4 == 0)
  */
 int dsa_indexer_score_topk(const void* q, const void* kv_cache, int64_t kv_batch_stride,
                            const void* wl, float w_scale, const void* freqs_cis,

@@ -10,6 +10,8 @@ sparse_attn_ref  follows reference/task1_v0_ref.py:5-24 op for op (fp32 einsums 
                  (all slots masked -> 0; q = 0 -> uniform weights incl. the sink; all
                  slots equal -> closed form; slot-permutation invariance; fp64 brute force).
 sparse_attn_fp64 independent per-row fp64 loop (small shapes only), used to pin the above.
+v_dim            sparse-MLA extension of both (keys = kv[..., :d_qk], values = kv[..., :v_dim]);
+                 pinned by the fp64 loop and by reducing to the reference when v_dim = d.
 Model / get_inputs / get_init_inputs  restate task1_v0_ref.py:27-55.
 """
 from __future__ import annotations
@@ -19,43 +21,51 @@ import torch
 import torch.nn as nn
 
 
-def sparse_attn_ref(q, kv, attn_sink, topk_idxs, softmax_scale):
-    """reference/task1_v0_ref.py:5-24."""
+def sparse_attn_ref(q, kv, attn_sink, topk_idxs, softmax_scale, v_dim=None):
+    """reference/task1_v0_ref.py:5-24. v_dim (an extension for sparse MLA; None = the
+    reference): the scores use kv[..., :d] with d = q's width, the output sums
+    kv[..., :v_dim] (the reference is v_dim = d = kv's width)."""
     b, m, h, _ = q.shape
     k = topk_idxs.shape[-1]
     keep = topk_idxs >= 0                                                  # :8
     rows = kv[torch.arange(b, device=q.device)[:, None, None].expand(b, m, k),
               topk_idxs.clamp(min=0).long()]                               # :9-11
     rows = rows.masked_fill(~keep.unsqueeze(-1), 0.0)                      # :12
-    logits = torch.einsum("bmhd,bmtd->bmht", q.float(), rows.float()) * softmax_scale  # :13
+    d = q.shape[-1]
+    krows = rows if rows.shape[-1] == d else rows[..., :d]
+    vrows = rows if v_dim is None else rows[..., :v_dim]
+    logits = torch.einsum("bmhd,bmtd->bmht", q.float(), krows.float()) * softmax_scale  # :13
     logits = logits.masked_fill(~keep.unsqueeze(2), float("-inf"))         # :14
     sink = attn_sink.float().view(1, 1, h, 1)                              # :15
     top = torch.maximum(torch.amax(logits, dim=-1, keepdim=True), sink)    # :16-17
     ex = torch.exp(logits - top).masked_fill(~keep.unsqueeze(2), 0.0)      # :18-19
     denom = ex.sum(dim=-1, keepdim=True) + torch.exp(sink - top)           # :20-21
-    out = torch.einsum("bmht,bmtd->bmhd", ex / denom, rows.float())        # :22-23
+    out = torch.einsum("bmht,bmtd->bmhd", ex / denom, vrows.float())       # :22-23
     return out.to(q.dtype)                                                 # :24
 
 
-def sparse_attn_fp64(q, kv, attn_sink, topk_idxs, softmax_scale) -> np.ndarray:
+def sparse_attn_fp64(q, kv, attn_sink, topk_idxs, softmax_scale, v_dim=None) -> np.ndarray:
     """Independent fp64 statement of the same maths, one (b, m, h) row at a time."""
     qn = q.double().cpu().numpy()
     kvn = kv.double().cpu().numpy()
+    kn = kvn[..., :qn.shape[-1]]
+    vn = kvn if v_dim is None else kvn[..., :v_dim]
     idx = topk_idxs.cpu().numpy()
     sink = attn_sink.double().cpu().numpy()
-    b, m, h, d = qn.shape
-    out = np.zeros((b, m, h, d))
+    b, m, h, _ = qn.shape
+    dv = vn.shape[-1]
+    out = np.zeros((b, m, h, dv))
     for bi in range(b):
         for mi in range(m):
             sel = [int(j) for j in idx[bi, mi] if j >= 0]
             for hi in range(h):
-                s = [float(np.dot(qn[bi, mi, hi], kvn[bi, j])) * softmax_scale for j in sel]
+                s = [float(np.dot(qn[bi, mi, hi], kn[bi, j])) * softmax_scale for j in sel]
                 mx = max(s + [sink[hi]])
                 e = [np.exp(v - mx) for v in s]
                 z = sum(e) + np.exp(sink[hi] - mx)
-                acc = np.zeros(d)
+                acc = np.zeros(dv)
                 for w, j in zip(e, sel):
-                    acc += (w / z) * kvn[bi, j]
+                    acc += (w / z) * vn[bi, j]
                 out[bi, mi, hi] = acc
     return out
 

@@ -1,0 +1,130 @@
+"""Sparse MLA (the attention of the configs[4] DSA layer) on the MI355X, through the C ABI,
+against the oracle's sparse_attn_ref with a value width (keys kv[..., :576], values
+kv[..., :512]) on the same GPU. Bar: bf16 within atol 1e-2 / rtol 1e-2; the fraction of
+bit-identical outputs is printed."""
+import pytest
+import torch
+
+from ascendc_kernel_amd import _native
+from ascendc_kernel_amd import task1_sparse_attn as t1
+from ascendc_kernel_amd import task2_indexer as t2
+from oracle import indexer as oix
+from oracle import sparse_attn as osa
+
+pytestmark = pytest.mark.gpu
+
+DQK, DV = 576, 512
+SCALE = DQK ** -0.5
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _compare(out, ref, name, atol=1e-2, rtol=1e-2):
+    o, r = out.float(), ref.float()
+    diff = (o - r).abs()
+    bad = diff > atol + rtol * r.abs()
+    exact = (out.view(torch.int16) == ref.view(torch.int16)).float().mean().item()
+    _say(f"[{name}] bit-exact {exact:.6f} max|diff| {diff.max().item():.3e} over tol {int(bad.sum())}")
+    assert not bad.any(), f"{name}: {int(bad.sum())} elements outside atol={atol} rtol={rtol}"
+    assert torch.isfinite(o).all()
+    return exact
+
+
+def _case(b, m, h, n_kv, topk, seed, masked=0.0, sink_scale=0.0, kv_dim=DQK, dev="cuda"):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, m, h, DQK, generator=g).to(torch.bfloat16)
+    kv = torch.randn(b, n_kv, kv_dim, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, n_kv, (b, m, topk), generator=g, dtype=torch.int32)
+    if masked:
+        idx[torch.rand(b, m, topk, generator=g) < masked] = -1
+    sink = torch.randn(h, generator=g) * sink_scale
+    return q.to(dev), kv.to(dev), idx.to(dev), sink.to(dev)
+
+
+CASES = [
+    # b, m, h, n_kv, topk, seed, masked, sink
+    (1, 24, 128, 300, 64, 1, 0.2, 1.0),
+    (2, 9, 64, 100, 33, 2, 0.0, 0.0),
+    (1, 5, 80, 2048, 2048, 3, 0.5, 0.5),
+    (1, 6, 128, 40, 1, 4, 0.0, 2.0),
+    (1, 12, 112, 500, 200, 5, 0.9, -1.0),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_mla_shapes_and_masks(gpu, case):
+    b, m, h, n_kv, topk, seed, masked, sink_scale = case
+    _say("mla case", case)
+    q, kv, idx, sink = _case(b, m, h, n_kv, topk, seed, masked, sink_scale)
+    out = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV)
+    ref = osa.sparse_attn_ref(q, kv, sink, idx, SCALE, v_dim=DV)
+    _compare(out, ref, f"mla{case}")
+
+
+def test_mla_masked_tokens_oob_and_wide_rows(gpu):
+    """Fully masked tokens give 0; indices >= n_kv count as masked; kv rows wider than 576."""
+    q, kv, idx, sink = _case(1, 6, 64, 50, 40, 6, 0.0, 1.0, kv_dim=640)
+    idx[0, 1] = -1
+    idx[0, 2, ::3] = 60
+    _say("mla masked/oob/wide")
+    out = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV)
+    ref = osa.sparse_attn_ref(q, kv, sink, torch.where(idx >= 50, -1, idx), SCALE, v_dim=DV)
+    _compare(out, ref, "mla-masked")
+    assert torch.count_nonzero(out[0, 1]) == 0
+
+
+def test_mla_drop_in_module(gpu):
+    """task1 Model with v_dim: the drop-in surface routes to the MLA kernel."""
+    q, kv, idx, sink = _case(1, 16, 128, 256, 128, 7, 0.1, 0.0)
+    m = t1.Model(128, DQK, v_dim=DV).to(gpu)
+    _say("mla module")
+    out = m(q, kv, idx.long())
+    ref = osa.sparse_attn_ref(q, kv, m.attn_sink, idx, m.softmax_scale, v_dim=DV)
+    _compare(out, ref, "mla-module")
+
+
+def test_full_shape_c5_mla_sampled(gpu):
+    """configs[4] attention: q[1,8192,128,576], kv[1,8192,576], top-2048 causal picks. The
+    kernel runs on the whole shape; the oracle checks every 32nd token (and the last)."""
+    _say("case c5 mla inputs")
+    q, kv, idx = t1.get_mla_inputs(device=gpu)
+    sink = torch.zeros(128, device=gpu)
+    _say("case c5 mla kernel")
+    out = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV)
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, 8192, 32), torch.tensor([8191])]).to(gpu)
+    _say("case c5 mla oracle")
+    ref = torch.cat([osa.sparse_attn_ref(q[:, rows[i:i + 32]], kv, sink, idx[:, rows[i:i + 32]], SCALE, v_dim=DV)
+                     for i in range(0, len(rows), 32)], dim=1)
+    exact = _compare(out[:, rows], ref, "c5-mla")
+    assert exact > 0.97
+
+
+def test_dsa_layer_indexer_then_mla(gpu):
+    """The two halves chained as in the DSA layer (smaller sequence): the indexer's int64
+    top-k (with -1 for masked picks) feeds the MLA kernel directly."""
+    seqlen, topk = 1024, 512
+    args = oix.IndexerArgs(max_batch_size=1, max_seq_len=seqlen, dim=7168, q_lora_rank=1536,
+                           rope_head_dim=64, index_n_heads=64, index_head_dim=128, index_topk=topk)
+    torch.manual_seed(51)
+    fr = oix.precompute_freqs_cis(64, seqlen, device=gpu)
+    kvc = torch.randn(1, seqlen, 128, dtype=torch.bfloat16).to(gpu)
+    ix = t2.Model(args, fr, kvc, 1).to(gpu)
+    g = torch.Generator().manual_seed(52)
+    with torch.no_grad():
+        for p in (ix.wq_b.weight, ix.weights_proj.weight):
+            p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(torch.bfloat16))
+    x = torch.randn(1, seqlen, 7168, generator=g).to(torch.bfloat16).to(gpu)
+    qr = torch.randn(1, seqlen, 1536, generator=g).to(torch.bfloat16).to(gpu)
+    _say("case dsa layer")
+    with torch.no_grad():
+        topk_idxs = ix(x, qr, 0, 0)
+    assert topk_idxs.dtype == torch.int64 and tuple(topk_idxs.shape) == (1, seqlen, topk)
+    qm = torch.randn(1, seqlen, 128, DQK, generator=g).to(torch.bfloat16).to(gpu)
+    kvm = torch.randn(1, seqlen, DQK, generator=g).to(torch.bfloat16).to(gpu)
+    attn = t1.Model(128, DQK, v_dim=DV).to(gpu)
+    out = attn(qm, kvm, topk_idxs)
+    ref = osa.sparse_attn_ref(qm, kvm, attn.attn_sink, topk_idxs, attn.softmax_scale, v_dim=DV)
+    _compare(out, ref, "dsa-layer")

@@ -102,3 +102,23 @@ def test_slot_permutation_invariance():
     a = osa.sparse_attn_ref(q, kv, sink, idx, 0.2).float()
     b = osa.sparse_attn_ref(q, kv, sink, idx[..., perm], 0.2).float()
     assert torch.allclose(a, b, atol=1e-2, rtol=2 ** -7)
+
+
+def test_value_width_extension():
+    """v_dim (sparse MLA): v_dim = d is the reference path itself; v_dim < d matches the
+    independent fp64 loop (keys = kv[..., :d_qk], values = kv[..., :v_dim])."""
+    g = torch.Generator().manual_seed(17)
+    q = torch.randn(1, 3, 4, 24, generator=g).to(torch.bfloat16)
+    kv = torch.randn(1, 10, 24, generator=g).to(torch.bfloat16)
+    idx = torch.randint(-1, 10, (1, 3, 6), generator=g, dtype=torch.int32)
+    sink = torch.randn(4, generator=g)
+    same = osa.sparse_attn_ref(q, kv, sink, idx, 0.2, v_dim=24)
+    assert torch.equal(same, osa.sparse_attn_ref(q, kv, sink, idx, 0.2))
+    got = osa.sparse_attn_ref(q, kv, sink, idx, 0.2, v_dim=16).float().numpy()
+    want = osa.sparse_attn_fp64(q, kv, sink, idx, 0.2, v_dim=16)
+    assert got.shape == (1, 3, 4, 16)
+    assert np.allclose(got, want, atol=1e-2, rtol=1e-2)
+    # keys wider than the query: only the first d_qk channels enter the scores
+    kv2 = torch.cat([kv, torch.randn(1, 10, 8, generator=g).to(torch.bfloat16)], dim=-1)
+    assert torch.equal(osa.sparse_attn_ref(q, kv2, sink, idx, 0.2, v_dim=16),
+                       osa.sparse_attn_ref(q, kv, sink, idx, 0.2, v_dim=16))
