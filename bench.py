@@ -7,7 +7,8 @@ replacement), inputs resident in HBM. One step = one forward call of the drop-in
 module (one kernel launch). value = algorithmic HBM bytes per call / time per call.
 
 Also reported: "task1_c4", the true-gather kernel at configs[3] (MFMA-bound: useful
-TFLOP/s and fraction of the dense bf16 peak), and "task2", the Task2 indexer at
+TFLOP/s and fraction of the dense bf16 peak), "dsa_layer_c5", the configs[4] DSA layer
+(wide indexer and sparse MLA), and "task2", the Task2 indexer at
 configs[2] (full Model.forward = two torch projections + the fused score/top-k
 kernel) and the fused kernel alone.
 
@@ -124,6 +125,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-task2", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the configs[3] true-gather leg")
+    ap.add_argument("--no-c5", action="store_true", help="skip the configs[4] DSA-layer leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run 5 plain device copies of 256 MiB (counter calibration for rocprofv3 --pmc)")
     a = ap.parse_args()
@@ -217,6 +219,60 @@ def main():
             "traffic": _traffic("sa_gather_kernel"),
         }
         del q4, kv4, idx4
+
+    # ---------------- DSA layer: wide indexer + sparse MLA
+    if not a.no_c5:
+        torch.cuda.empty_cache()
+        torch.manual_seed(42)
+        init5 = t2.get_c5_init_inputs(device=dev)
+        ix5 = t2.Model(*init5).to(dev)
+        g5 = torch.Generator().manual_seed(5)
+        with torch.no_grad():
+            for p5 in (ix5.wq_b.weight, ix5.weights_proj.weight):
+                p5.copy_((torch.randn(p5.shape, generator=g5) * 0.02).to(torch.bfloat16))
+        x5, qr5, sp5, off5 = t2.get_c5_inputs(device=dev)
+        n5 = max(3, a.steps // 10)
+        with torch.no_grad():
+            for _ in range(2):
+                ix5(x5, qr5, sp5, off5)
+            torch.cuda.synchronize()
+            ms_ix = _events_time(torch, lambda: ix5(x5, qr5, sp5, off5), n5, stream)
+            q5 = torch.nn.functional.linear(qr5, ix5.wq_b.weight).unflatten(-1, (64, 128)).contiguous()
+            wl5 = torch.nn.functional.linear(x5, ix5.weights_proj.weight)
+            fr5 = ix5.freqs_cis[:8192]
+            kix = lambda: _native.indexer_score_topk(q5, ix5.kv_cache, wl5, 128 ** -0.5 * 64 ** -0.5, fr5,
+                                                     64, 8192, 2048, 1, True, 0)
+            kix()
+            torch.cuda.synchronize()
+            ms_ixk = _events_time(torch, kix, n5, stream)
+        del x5, qr5, q5, wl5
+        torch.cuda.empty_cache()
+        qm, kvm, idxm = t1.get_mla_inputs(device=dev)
+        mla = t1.Model(128, 576, v_dim=512).to(dev)
+        with torch.no_grad():
+            for _ in range(2):
+                mla(qm, kvm, idxm)
+            torch.cuda.synchronize()
+            ms_mla = _events_time(torch, lambda: mla(qm, kvm, idxm), n5, stream)
+        valid_m = int((idxm >= 0).sum().item())
+        flop_m = valid_m * 128 * (576 + 512) * 2
+        bytes_m = qm.numel() * 2 + 8192 * 128 * 512 * 2 + kvm.numel() * 2 + idxm.numel() * 4 + 128 * 4
+        score_flop5 = 2 * 64 * 128 * (8192 * 8193 // 2)
+        result["dsa_layer_c5"] = {
+            "workload": "configs[4]: indexer 64x128 from qr[1,8192,1536] / x[1,8192,7168], kv_cache[1,8192,128], "
+                        "causal top-2048 (ratio 1, rope_head_dim 64, W ~ N(0,0.02)); sparse MLA q[1,8192,128,576], "
+                        "latent kv[1,8192,576], d_v 512, causal top-2048 picks",
+            "indexer_model_us": round(ms_ix * 1e3, 1),
+            "indexer_kernel_us": round(ms_ixk * 1e3, 1),
+            "indexer_useful_score_TFLOPs": round(score_flop5 / (ms_ixk * 1e-3) / 1e12, 1),
+            "mla_kernel": "sa_mla_kernel",
+            "mla_us": round(ms_mla * 1e3, 1),
+            "mla_useful_TFLOPs": round(flop_m / (ms_mla * 1e-3) / 1e12, 1),
+            "mla_mfma_frac": round(flop_m / (ms_mla * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "mla_algorithmic_bytes": bytes_m,
+            "mla_GBps": round(bytes_m / (ms_mla * 1e-3) / 1e9, 1),
+        }
+        del qm, kvm, idxm
 
     # ---------------- Task2
     if not a.no_task2:

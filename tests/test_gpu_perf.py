@@ -68,3 +68,30 @@ def test_task1_c4_faster_than_torch_path(gpu):
     r_us = _median_us(ref, reps=3, warm=1)
     print(f"[perf c4] kernel {k_us:.1f} us, torch path {r_us:.1f} us, x{r_us / k_us:.1f}", flush=True)
     assert k_us < r_us
+
+
+def test_dsa_layer_c5_faster_than_torch_path(gpu):
+    """the indexer Model.forward at full size; sparse MLA on 256 tokens of the
+    full-size inputs (the torch path's gathered rows for all 8192 tokens would be ~40 GB)."""
+    torch.manual_seed(42)
+    init = t2.get_c5_init_inputs(device=gpu)
+    m = t2.Model(*init).to(gpu)
+    r = oix.IndexerRef(*init).to(gpu)
+    r.wq_b.weight.data.copy_(m.wq_b.weight.data)
+    r.weights_proj.weight.data.copy_(m.weights_proj.weight.data)
+    x, qr, sp, off = t2.get_c5_inputs(device=gpu)
+    with torch.no_grad():
+        k_us = _median_us(lambda: m(x, qr, sp, off), reps=5)
+        r_us = _median_us(lambda: r(x, qr, sp, off), reps=3, warm=1)
+    print(f"[perf c5 indexer] Model.forward {k_us:.1f} us, torch path {r_us:.1f} us, x{r_us / k_us:.1f}", flush=True)
+    assert k_us < r_us
+    del x, qr
+    q, kv, idx = t1.get_mla_inputs(device=gpu)
+    attn = t1.Model(128, 576, v_dim=512).to(gpu)
+    sl = slice(4096, 4096 + 256)
+    qs, ids = q[:, sl].contiguous(), idx[:, sl].contiguous()
+    k_us = _median_us(lambda: attn(qs, kv, ids), reps=10)
+    r_us = _median_us(lambda: osa.sparse_attn_ref(qs, kv, attn.attn_sink, ids, attn.softmax_scale, v_dim=512),
+                      reps=3, warm=1)
+    print(f"[perf c5 mla, 256 tokens] kernel {k_us:.1f} us, torch path {r_us:.1f} us, x{r_us / k_us:.1f}", flush=True)
+    assert k_us < r_us
