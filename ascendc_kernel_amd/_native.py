@@ -30,6 +30,8 @@ EXPORTS = (
     "dsa_sparse_mla_fwd",
     "dsa_indexer_rope",
     "dsa_indexer_score_topk",
+    "dsa_indexer_workspace_bytes",
+    "dsa_indexer_score_topk_ws",
     "dsa_indexer_scores",
 )
 
@@ -83,6 +85,13 @@ def load() -> ctypes.CDLL:
         _c_vp, _c_vp, _c_i64, _c_vp, ctypes.c_float, _c_vp, ctypes.c_int32, _c_vp,
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
         ctypes.c_int32, _c_i64, _c_vp]
+    lib.dsa_indexer_workspace_bytes.restype = ctypes.c_int64
+    lib.dsa_indexer_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]
+    lib.dsa_indexer_score_topk_ws.restype = ctypes.c_int
+    lib.dsa_indexer_score_topk_ws.argtypes = [
+        _c_vp, _c_vp, _c_i64, _c_vp, ctypes.c_float, _c_vp, ctypes.c_int32, _c_vp,
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        ctypes.c_int32, _c_i64, _c_vp, _c_i64, _c_vp]
     lib.dsa_indexer_scores.restype = ctypes.c_int
     lib.dsa_indexer_scores.argtypes = [
         _c_vp, _c_vp, _c_i64, _c_vp, ctypes.c_float, _c_vp, ctypes.c_int32, _c_vp,
@@ -202,11 +211,13 @@ def _freqs_view(freqs_cis: torch.Tensor, s: int, rd: int) -> torch.Tensor:
 def indexer_score_topk(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor,
                        w_scale: float, freqs_cis: Optional[torch.Tensor], rope_head_dim: int,
                        n_cand: int, k_out: int, ratio: int, causal: bool, offset: int,
-                       rope_mode: int = DSA_ROPE_TORCH_ROCM) -> torch.Tensor:
+                       rope_mode: int = DSA_ROPE_TORCH_ROCM, use_workspace: bool = True) -> torch.Tensor:
     """Task2 score + mask + top-k; returns int64 [b, s, k_out].
 
     q: bf16 [b, s, h, d] (contiguous); kv_cache: bf16 [>=b, >=n_cand, d] with unit
     row stride; wl: bf16 [b, s, h]; freqs_cis: complex64 rows for the s positions.
+    When the configuration takes a workspace (64 heads x 128) it is allocated from
+    torch's caching allocator and passed in (use_workspace=False: the single-kernel path).
     """
     lib = load()
     b, s, h, d = q.shape
@@ -223,6 +234,16 @@ def indexer_score_topk(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor
     fr = _freqs_view(freqs_cis, s, rope_head_dim) if freqs_cis is not None else None
     _require_gpu(q, kv_cache, wl, *([fr] if fr is not None else []))
     out = torch.empty(b, s, k_out, dtype=torch.int64, device=q.device)
+    ws_bytes = int(lib.dsa_indexer_workspace_bytes(b, s, h, d, n_cand)) if use_workspace else 0
+    if ws_bytes > 0:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        rc = lib.dsa_indexer_score_topk_ws(
+            q.data_ptr(), kv_cache.data_ptr(), kv_cache.stride(0), wl.data_ptr(), float(w_scale),
+            fr.data_ptr() if fr is not None else None, int(rope_mode), out.data_ptr(),
+            b, s, h, d, rope_head_dim, n_cand, k_out, ratio, 1 if causal else 0, int(offset),
+            ws.data_ptr(), ws_bytes, _stream(q))
+        _check("dsa_indexer_score_topk_ws", rc)
+        return out
     rc = lib.dsa_indexer_score_topk(
         q.data_ptr(), kv_cache.data_ptr(), kv_cache.stride(0), wl.data_ptr(), float(w_scale),
         fr.data_ptr() if fr is not None else None, int(rope_mode), out.data_ptr(),

@@ -458,11 +458,13 @@ extern "C" int dsa_indexer_rope(void* q, const void* freqs_cis, int64_t b, int64
   return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
 }
 
+int64_t dsa_indexer_wide_workspace_bytes(int64_t b, int64_t s, int64_t n_cand);
 int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batch_stride,
                             const void* wl, float w_scale, const void* freqs_cis,
                             int32_t rope_mode, int64_t* out, uint16_t* scores, int64_t b,
                             int64_t s, int64_t rd, int64_t n_cand, int64_t k_out,
-                            int64_t ratio, int32_t causal, int64_t offset, hipStream_t stream);
+                            int64_t ratio, int32_t causal, int64_t offset, void* workspace,
+                            int64_t workspace_bytes, hipStream_t stream);
 
 namespace {
 
@@ -470,7 +472,7 @@ int launch_ix(const void* q, const void* kv_cache, int64_t kv_batch_stride, cons
               float w_scale, const void* freqs_cis, int32_t rope_mode, int64_t* out,
               uint16_t* scores, int64_t b, int64_t s, int64_t h, int64_t d, int64_t rd,
               int64_t n_cand, int64_t k_out, int64_t ratio, int32_t causal, int64_t offset,
-              void* stream) {
+              void* workspace, int64_t workspace_bytes, void* stream) {
   if (b < 0 || s < 0 || h <= 0 || d <= 0 || n_cand < 1 || k_out < 1 || ratio < 1)
     return DSA_ERR_SHAPE;
   if (k_out > n_cand) return DSA_ERR_SHAPE;
@@ -490,10 +492,11 @@ int launch_ix(const void* q, const void* kv_cache, int64_t kv_batch_stride, cons
       (freqs_cis != nullptr && ((uintptr_t)freqs_cis & 7u)))
     return DSA_ERR_ALIGN;
 
+  if (workspace_bytes < 0) return DSA_ERR_SHAPE;
   if (wide)
     return dsa_indexer_wide_launch(q, kv_cache, kv_batch_stride, wl, w_scale, freqs_cis, rope_mode,
                                    out, scores, b, s, rd, n_cand, k_out, ratio, causal, offset,
-                                   (hipStream_t)stream);
+                                   workspace, workspace_bytes, (hipStream_t)stream);
 
   IxParams p;
   p.q = (const uint16_t*)q;
@@ -544,7 +547,27 @@ extern "C" int dsa_indexer_score_topk(const void* q, const void* kv_cache, int64
                                       int64_t offset, void* stream) {
   if (out == nullptr && b > 0 && s > 0) return DSA_ERR_NULL;
   return launch_ix(q, kv_cache, kv_batch_stride, wl, w_scale, freqs_cis, rope_mode, out, nullptr,
-                   b, s, h, d, rd, n_cand, k_out, ratio, causal, offset, stream);
+                   b, s, h, d, rd, n_cand, k_out, ratio, causal, offset, nullptr, 0, stream);
+}
+
+extern "C" int64_t dsa_indexer_workspace_bytes(int64_t b, int64_t s, int64_t h, int64_t d,
+                                               int64_t n_cand) {
+  if (b < 0 || s < 0 || n_cand < 0) return -1;
+  if (h == 64 && d == 128) return dsa_indexer_wide_workspace_bytes(b, s, n_cand);
+  return 0;
+}
+
+extern "C" int dsa_indexer_score_topk_ws(const void* q, const void* kv_cache, int64_t kv_batch_stride,
+                                         const void* wl, float w_scale, const void* freqs_cis,
+                                         int32_t rope_mode, int64_t* out, int64_t b, int64_t s,
+                                         int64_t h, int64_t d, int64_t rd, int64_t n_cand,
+                                         int64_t k_out, int64_t ratio, int32_t causal,
+                                         int64_t offset, void* workspace, int64_t workspace_bytes,
+                                         void* stream) {
+  if (out == nullptr && b > 0 && s > 0) return DSA_ERR_NULL;
+  return launch_ix(q, kv_cache, kv_batch_stride, wl, w_scale, freqs_cis, rope_mode, out, nullptr,
+                   b, s, h, d, rd, n_cand, k_out, ratio, causal, offset, workspace, workspace_bytes,
+                   stream);
 }
 
 extern "C" int dsa_indexer_scores(const void* q, const void* kv_cache, int64_t kv_batch_stride,
@@ -554,5 +577,5 @@ extern "C" int dsa_indexer_scores(const void* q, const void* kv_cache, int64_t k
                                   int32_t causal, void* stream) {
   if (scores == nullptr && b > 0 && s > 0) return DSA_ERR_NULL;
   return launch_ix(q, kv_cache, kv_batch_stride, wl, w_scale, freqs_cis, rope_mode, nullptr,
-                   (uint16_t*)scores, b, s, h, d, rd, n_cand, 1, ratio, causal, 0, stream);
+                   (uint16_t*)scores, b, s, h, d, rd, n_cand, 1, ratio, causal, 0, nullptr, 0, stream);
 }

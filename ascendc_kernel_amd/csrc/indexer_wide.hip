@@ -54,7 +54,9 @@ struct WideParams {
   const float* freqs;   // [S, rd/2, 2] (rows from start_pos) or nullptr
   int32_t rope_mode;
   int64_t* out;         // [B, S, K]
-  uint16_t* scores;     // optional [B, S, T] bf16 score dump (masked -inf); then no top-k
+  uint16_t* gkeys;      // if set: per-candidate results go to this [B*S, T] buffer instead of
+                        // LDS and the kernel ends after the scores (no top-k)
+  int32_t graw;         // 1: gkeys gets the bf16 scores (masked -inf); 0: 16-bit order keys
   int32_t B, S, rd, T, K, ratio, causal;
   int64_t offset;
   int32_t groups;       // ceil(S / kTok)
@@ -138,6 +140,164 @@ __device__ __forceinline__ int find_bin64(const uint32_t* hist, int lane, uint32
   const int src = m ? (int)__builtin_ctzll(m) : 0;
   gt = __shfl(fgt, src, 64);
   return __shfl(fb, src, 64);
+}
+
+// hist[bin] += 1 for the active lanes of a wave, one LDS atomic per distinct bin
+// (the high bytes of a row's order keys fall into a handful of bins).
+__device__ __forceinline__ void hist_add_grouped(uint32_t* hist, uint32_t bin, bool active, int lane) {
+  uint64_t m = __ballot(active);
+  while (m) {
+    const int leader = (int)__builtin_ctzll(m);
+    const uint32_t lb = (uint32_t)__shfl((int)bin, leader, 64);
+    const uint64_t same = __ballot(active && bin == lb);
+    if (lane == leader) atomicAdd(&hist[lb], (uint32_t)__builtin_popcountll(same));
+    m &= ~same;
+  }
+}
+
+// Top-K of one row of 16-bit order keys held in LDS (keys[0..nv) are the valid
+// candidates), by `nthr` threads (thread index tt, waves of 64) of a workgroup
+// whose every thread calls this (it contains __syncthreads): two-pass 8-bit radix
+// select of the K-th key, compaction of the picks ([keys > k-th] then the first
+// [== k-th] in index order), bitonic sort of (key, ~index) composites descending,
+// int64 output (index + offset; -1 for picks beyond the valid candidates).
+// hist: 512 words, sel: 4 words, sb: psort words of LDS.
+__device__ void select_topk_row(const uint16_t* keys, int nv, int K, int psort, uint32_t* hist,
+                                int32_t* sel, uint32_t* sb, int tt, int nthr, int64_t* out_row,
+                                int64_t offset) {
+  const int lane = tt & 63;
+  const int nw = nthr >> 6, wv = tt >> 6;
+  const bool selecting = nv > K;
+  uint32_t* h1 = hist;
+  uint32_t* h2 = hist + 256;
+  for (int i = tt; i < 512; i += nthr) h1[i] = 0u;
+  __syncthreads();
+  if (selecting)
+    for (int c0 = wv * 64; c0 < nv; c0 += nthr) {
+      const int c = c0 + lane;
+      hist_add_grouped(h1, c < nv ? (uint32_t)keys[c] >> 8 : 0u, c < nv, lane);
+    }
+  __syncthreads();
+  if (selecting && tt < 64) {
+    uint32_t gt;
+    const int b1 = find_bin64(h1, lane, (uint32_t)K, gt);
+    if (lane == 0) {
+      sel[0] = b1;
+      sel[1] = (int32_t)gt;
+    }
+  }
+  __syncthreads();
+  const int b1 = sel[0];
+  if (selecting)
+    for (int c = tt; c < nv; c += nthr) {
+      const uint32_t u = keys[c];
+      if ((int)(u >> 8) == b1) atomicAdd(&h2[u & 255u], 1u);
+    }
+  __syncthreads();
+  if (selecting && tt < 64) {
+    uint32_t gt;
+    const uint32_t above = (uint32_t)sel[1];
+    const int b0 = find_bin64(h2, lane, (uint32_t)K - above, gt);
+    if (lane == 0) {
+      sel[2] = b0;
+      sel[3] = (int32_t)(above + gt);
+    }
+  }
+  __syncthreads();
+  const int count = selecting ? K : nv;  // picks that are real candidates
+  // Compaction: wave wv scans candidates [wv * chunk, (wv + 1) * chunk) twice, first
+  // counting its picks (h1 is free again) and then writing them after the picks of
+  // the lower waves, in index order.
+  const uint32_t kth = ((uint32_t)b1 << 8) | (uint32_t)sel[2];
+  const uint32_t n_gt = (uint32_t)sel[3];
+  const int chunk = (nv + 64 * nw - 1) / (64 * nw) * 64;
+  const int c_beg = wv * chunk, c_end = min(nv, c_beg + chunk);
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  __syncthreads();  // everyone has read sel before h1 is reused
+  if (selecting) {
+    uint32_t ng = 0, ne = 0;
+    for (int c0 = c_beg; c0 < c_end; c0 += 64) {
+      const int c = c0 + lane;
+      const uint32_t u = c < c_end ? (uint32_t)keys[c] : 0u;
+      ng += __builtin_popcountll(__ballot(c < c_end && u > kth));
+      ne += __builtin_popcountll(__ballot(c < c_end && u == kth));
+    }
+    if (lane == 0) {
+      h1[wv] = ng;
+      h1[8 + wv] = ne;
+    }
+  }
+  __syncthreads();
+  if (selecting) {
+    uint32_t run_gt = 0, run_eq = 0;
+    for (int w = 0; w < wv; ++w) {
+      run_gt += h1[w];
+      run_eq += h1[8 + w];
+    }
+    const uint32_t need_eq = (uint32_t)K - n_gt;
+    for (int c0 = c_beg; c0 < c_end; c0 += 64) {
+      const int c = c0 + lane;
+      const uint32_t u = c < c_end ? (uint32_t)keys[c] : 0u;
+      const bool g = c < c_end && u > kth;
+      const bool e = c < c_end && u == kth;
+      const uint64_t mg = __ballot(g), me = __ballot(e);
+      const uint32_t comp = (u << 16) | (0xffffu - (uint32_t)c);
+      if (g) sb[run_gt + __builtin_popcountll(mg & below)] = comp;
+      if (e) {
+        const uint32_t r = run_eq + __builtin_popcountll(me & below);
+        if (r < need_eq) sb[n_gt + r] = comp;
+      }
+      run_gt += __builtin_popcountll(mg);
+      run_eq += __builtin_popcountll(me);
+    }
+  } else {
+    for (int c = tt; c < nv; c += nthr) sb[c] = ((uint32_t)keys[c] << 16) | (0xffffu - (uint32_t)c);
+  }
+  for (int j = count + tt; j < psort; j += nthr) sb[j] = 0u;  // sorts last
+  __syncthreads();
+  // Bitonic sort, descending. Wave wv owns elements [wv * seg, (wv + 1) * seg); the
+  // steps whose pairs stay inside a segment (stride < seg) run with wave-level
+  // ordering only, the others between workgroup barriers.
+  const int seg = psort / nw;
+  for (int size = 2; size <= psort; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const bool cross = stride >= seg || seg < 128;
+      if (cross) {
+        __syncthreads();
+        for (int i = tt; i < (psort >> 1); i += nthr) {
+          const int lo = 2 * i - (i & (stride - 1));
+          const int hi = lo + stride;
+          const bool desc = (lo & size) == 0;
+          const uint32_t x = sb[lo], z = sb[hi];
+          if ((x < z) == desc) {
+            sb[lo] = z;
+            sb[hi] = x;
+          }
+        }
+        __syncthreads();
+      } else {
+        for (int i = wv * (seg >> 1) + lane; i < (wv + 1) * (seg >> 1); i += 64) {
+          const int lo = 2 * i - (i & (stride - 1));
+          const int hi = lo + stride;
+          const bool desc = (lo & size) == 0;
+          const uint32_t x = sb[lo], z = sb[hi];
+          if ((x < z) == desc) {
+            sb[lo] = z;
+            sb[hi] = x;
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+  }
+  __syncthreads();
+  if (out_row != nullptr)
+    for (int j = tt; j < K; j += nthr) {
+      const uint32_t comp = sb[j];
+      const int64_t c = (int64_t)(0xffffu - (comp & 0xffffu));
+      out_row[j] = (j < count) ? c + offset : (int64_t)-1;
+    }
 }
 
 __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
@@ -237,7 +397,7 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
 #pragma unroll
   for (int m = 0; m < 8; ++m) asm volatile("" ::"v"(wlo[m]), "v"(whi[m]));
 
-  const bool dump = p.scores != nullptr;
+  uint16_t* gdst = (p.gkeys != nullptr && tok_ok) ? p.gkeys + row_bt * p.T : nullptr;
   float t0val = 0.f;  // even-head total of the previous tile (y == 0 waves, upper lanes)
   // Keys of tile n-1: even + odd totals -> bf16 -> order key (or raw bits when dumping).
   auto finalize = [&](int n) {
@@ -246,7 +406,11 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
       uint32_t sc = f2bf(tot);
       if (p.causal) sc = f2bf(bf2f(sc) + 0.0f);  // the reference adds the 0 / -inf mask
       const int c = kTileC * n + col;
-      if (c < nv) mykeys[c] = (uint16_t)(dump ? sc : order_key16(sc));
+      if (c < nv) {
+        const uint16_t v = (uint16_t)(p.graw ? sc : order_key16(sc));
+        if (gdst != nullptr) gdst[c] = v;
+        else mykeys[c] = v;
+      }
     }
   };
 
@@ -292,119 +456,85 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
   __syncthreads();
 
   const int tt = y * 64 + lane;  // thread of the token (0..127)
-  if (dump) {
-    if (tok_ok) {
-      uint16_t* dst = p.scores + row_bt * p.T;
-      for (int c = tt; c < p.T; c += 128) dst[c] = c < nv ? mykeys[c] : (uint16_t)0xff80u;
-    }
+  if (p.gkeys != nullptr) {
+    if (p.graw && gdst != nullptr)  // score dump: never-valid candidates are -inf
+      for (int c = nv + tt; c < p.T; c += 128) gdst[c] = (uint16_t)0xff80u;
     return;
   }
 
-  // ---------------- top-K of the token: radix select, compaction, bitonic sort
-  const int K = p.K;
-  const bool selecting = nv > K;
-  uint32_t* h1 = hist + tl * 512;
-  uint32_t* h2 = h1 + 256;
-  for (int i = tt; i < 512; i += 128) h1[i] = 0u;
-  __syncthreads();
-  if (selecting)
-    for (int c = tt; c < nv; c += 128) atomicAdd(&h1[mykeys[c] >> 8], 1u);
-  __syncthreads();
-  if (selecting && y == 0) {
-    uint32_t gt;
-    const int b1 = find_bin64(h1, lane, (uint32_t)K, gt);
-    if (lane == 0) {
-      sel[tl * 4 + 0] = b1;
-      sel[tl * 4 + 1] = (int32_t)gt;
-    }
+  select_topk_row(mykeys, nv, p.K, p.psort, hist + tl * 512, sel + tl * 4, sortbuf + tl * p.psort, tt, 128,
+                  tok_ok ? p.out + row_bt * p.K : nullptr, p.offset);
+}
+
+
+// Top-K of rows of 16-bit order keys written by ix_wide_kernel: one workgroup
+// (256 threads) per token row.
+struct SelParams {
+  const uint16_t* keys;  // [B*S, T]
+  int64_t* out;          // [B*S, K]
+  int32_t S, T, K, ratio, causal, psort;
+  int64_t offset;
+};
+
+__global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint32_t* sortbuf = reinterpret_cast<uint32_t*>(smem);   // [psort]
+  uint32_t* hist = sortbuf + p.psort;                       // [512]
+  int32_t* sel = reinterpret_cast<int32_t*>(hist + 512);    // [4]
+  uint16_t* keys = reinterpret_cast<uint16_t*>(sel + 4);    // [T] (8-byte aligned)
+  const int64_t row = blockIdx.x;
+  const int t = (int)(row % p.S);
+  int nv = p.T;
+  if (p.causal) {
+    nv = (t + 1) / p.ratio;
+    if (nv > p.T) nv = p.T;
+  }
+  // The row in 8-byte pieces (T % 4 == 0), all loads of a thread issued before its
+  // stores: T <= 8192 keys = at most 8 pieces per thread.
+  const uint2* src = reinterpret_cast<const uint2*>(p.keys + row * p.T);
+  uint2* dst = reinterpret_cast<uint2*>(keys);
+  const int nq = (nv + 3) >> 2;
+  uint2 v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = (int)threadIdx.x + 256 * j;
+    v[j] = i < nq ? src[i] : uint2{0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = (int)threadIdx.x + 256 * j;
+    if (i < nq) dst[i] = v[j];
   }
   __syncthreads();
-  const int b1 = sel[tl * 4 + 0];
-  if (selecting)
-    for (int c = tt; c < nv; c += 128) {
-      const uint32_t u = mykeys[c];
-      if ((int)(u >> 8) == b1) atomicAdd(&h2[u & 255u], 1u);
-    }
-  __syncthreads();
-  if (selecting && y == 0) {
-    uint32_t gt;
-    const uint32_t above = (uint32_t)sel[tl * 4 + 1];
-    const int b0 = find_bin64(h2, lane, (uint32_t)K - above, gt);
-    if (lane == 0) {
-      sel[tl * 4 + 2] = b0;
-      sel[tl * 4 + 3] = (int32_t)(above + gt);
-    }
-  }
-  __syncthreads();
-  uint32_t* sb = sortbuf + tl * p.psort;
-  const int count = selecting ? K : nv;  // picks that are real candidates
-  if (selecting) {
-    if (y == 0) {
-      const uint32_t kth = ((uint32_t)b1 << 8) | (uint32_t)sel[tl * 4 + 2];
-      const uint32_t n_gt = (uint32_t)sel[tl * 4 + 3];
-      const uint32_t need_eq = (uint32_t)K - n_gt;
-      uint32_t run_gt = 0, run_eq = 0;
-      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-      for (int c0 = 0; c0 < nv; c0 += 64) {
-        const int c = c0 + lane;
-        const uint32_t u = c < nv ? (uint32_t)mykeys[c] : 0u;
-        const bool g = c < nv && u > kth;
-        const bool e = c < nv && u == kth;
-        const uint64_t mg = __ballot(g), me = __ballot(e);
-        const uint32_t comp = (u << 16) | (0xffffu - (uint32_t)c);
-        if (g) sb[run_gt + __builtin_popcountll(mg & below)] = comp;
-        if (e) {
-          const uint32_t r = run_eq + __builtin_popcountll(me & below);
-          if (r < need_eq) sb[n_gt + r] = comp;
-        }
-        run_gt += __builtin_popcountll(mg);
-        run_eq += __builtin_popcountll(me);
-      }
-    }
-  } else {
-    for (int c = tt; c < nv; c += 128) sb[c] = ((uint32_t)mykeys[c] << 16) | (0xffffu - (uint32_t)c);
-  }
-  for (int j = count + tt; j < p.psort; j += 128) sb[j] = 0u;  // sorts last
-  __syncthreads();
-  // Bitonic sort, descending, of psort entries per token (128 threads each).
-  for (int size = 2; size <= p.psort; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tt; i < (p.psort >> 1); i += 128) {
-        const int lo = 2 * i - (i & (stride - 1));
-        const int hi = lo + stride;
-        const bool desc = (lo & size) == 0;
-        const uint32_t a = sb[lo], c = sb[hi];
-        if ((a < c) == desc) {
-          sb[lo] = c;
-          sb[hi] = a;
-        }
-      }
-      __syncthreads();
-    }
-  }
-  if (tok_ok) {
-    int64_t* dst = p.out + row_bt * K;
-    for (int j = tt; j < K; j += 128) {
-      const uint32_t comp = sb[j];
-      const int64_t c = (int64_t)(0xffffu - (comp & 0xffffu));
-      dst[j] = (j < count) ? c + p.offset : (int64_t)-1;
-    }
-  }
+  select_topk_row(keys, nv, p.K, p.psort, hist, sel, sortbuf, threadIdx.x, 256, p.out + row * p.K,
+                  p.offset);
 }
 
 }  // namespace
 
 // Called by the indexer entry points for h == 64, d == 128 (checks common to both
 // configurations are done by the caller).
+int64_t dsa_indexer_wide_workspace_bytes(int64_t b, int64_t s, int64_t n_cand) {
+  return b * s * n_cand * 2;  // one 16-bit order key per (token, candidate)
+}
+
+// With a workspace of at least dsa_indexer_wide_workspace_bytes: the score kernel
+// writes order keys to it and ix_select_kernel ranks them (one workgroup per
+// token). Without: one fused kernel keeps the keys of 4 tokens in LDS. With
+// `scores`: the score kernel writes the bf16 scores there and nothing is ranked.
 int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batch_stride,
                             const void* wl, float w_scale, const void* freqs_cis,
                             int32_t rope_mode, int64_t* out, uint16_t* scores, int64_t b,
                             int64_t s, int64_t rd, int64_t n_cand, int64_t k_out,
-                            int64_t ratio, int32_t causal, int64_t offset, hipStream_t stream) {
+                            int64_t ratio, int32_t causal, int64_t offset, void* workspace,
+                            int64_t workspace_bytes, hipStream_t stream) {
   // The head-sum order reproduced here is torch's for a candidate count that is a
   // multiple of 4 (its reduction kernel vectorizes the output by 4 then).
   if (n_cand > kMaxT || (n_cand % 4) != 0) return DSA_ERR_UNSUPPORTED;
   if (k_out > kMaxK) return DSA_ERR_UNSUPPORTED;
+  const bool two_pass = scores == nullptr && workspace != nullptr &&
+                        workspace_bytes >= dsa_indexer_wide_workspace_bytes(b, s, n_cand);
+  if (workspace != nullptr && ((uintptr_t)workspace & 15u)) return DSA_ERR_ALIGN;
   WideParams p;
   p.q = (const uint16_t*)q;
   p.kv = (const uint16_t*)kv_cache;
@@ -414,7 +544,8 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
   p.freqs = (const float*)freqs_cis;
   p.rope_mode = rope_mode;
   p.out = out;
-  p.scores = scores;
+  p.gkeys = scores != nullptr ? scores : (two_pass ? (uint16_t*)workspace : nullptr);
+  p.graw = scores != nullptr ? 1 : 0;
   p.B = (int32_t)b;
   p.S = (int32_t)s;
   p.rd = (int32_t)rd;
@@ -424,18 +555,43 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
   p.causal = causal ? 1 : 0;
   p.offset = offset;
   p.groups = (int32_t)((s + kTok - 1) / kTok);
-  p.tpad = (int32_t)((n_cand + kTileC - 1) / kTileC * kTileC);
   int ps = 1;
   while (ps < k_out) ps <<= 1;
   p.psort = ps;
-  const size_t smem = (size_t)kTok * p.tpad * 2 + (size_t)kRingW * 8192 + 2 * kTok * kTileC * 4 +
-                      kTok * 512 * 4 + kTok * 4 * 4;
+  size_t smem;
+  if (p.gkeys != nullptr) {
+    p.tpad = 0;  // no key rows in LDS
+    smem = (size_t)kRingW * 8192 + 2 * kTok * kTileC * 4 + kTok * 512 * 4 + kTok * 4 * 4;
+  } else {
+    p.tpad = (int32_t)((n_cand + kTileC - 1) / kTileC * kTileC);
+    smem = (size_t)kTok * p.tpad * 2 + (size_t)kRingW * 8192 + 2 * kTok * kTileC * 4 +
+           kTok * 512 * 4 + kTok * 4 * 4;
+  }
   if (smem > 160 * 1024) return DSA_ERR_UNSUPPORTED;
   if (hipFuncSetAttribute((const void*)ix_wide_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)smem) != hipSuccess)
     return DSA_ERR_LAUNCH;
   const int64_t blocks = b * p.groups;
-  if (blocks > INT32_MAX) return DSA_ERR_SHAPE;
+  if (blocks > INT32_MAX || b * s > INT32_MAX) return DSA_ERR_SHAPE;
   hipLaunchKernelGGL(ix_wide_kernel, dim3((unsigned)blocks), dim3(512), smem, stream, p);
-  return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+  if (hipGetLastError() != hipSuccess) return DSA_ERR_LAUNCH;
+  if (two_pass) {
+    SelParams sp;
+    sp.keys = (const uint16_t*)workspace;
+    sp.out = out;
+    sp.S = p.S;
+    sp.T = p.T;
+    sp.K = p.K;
+    sp.ratio = p.ratio;
+    sp.causal = p.causal;
+    sp.psort = p.psort;
+    sp.offset = offset;
+    const size_t smem2 = (size_t)ps * 4 + 512 * 4 + 16 + (size_t)((n_cand + 7) / 8 * 8) * 2;
+    if (hipFuncSetAttribute((const void*)ix_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)smem2) != hipSuccess)
+      return DSA_ERR_LAUNCH;
+    hipLaunchKernelGGL(ix_select_kernel, dim3((unsigned)(b * s)), dim3(256), smem2, stream, sp);
+    if (hipGetLastError() != hipSuccess) return DSA_ERR_LAUNCH;
+  }
+  return DSA_OK;
 }

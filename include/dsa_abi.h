@@ -142,6 +142,29 @@ int dsa_indexer_score_topk(const void* q, const void* kv_cache, int64_t kv_batch
                            int64_t ratio, int32_t causal, int64_t offset, void* stream);
 
 /*
+ * Workspace for dsa_indexer_score_topk_ws, in bytes (0: the configuration needs none;
+ * -1: invalid sizes). For h == 64, d == 128 it is b * s * n_cand * 2 (one 16-bit order
+ * key per token and candidate).
+ */
+int64_t dsa_indexer_workspace_bytes(int64_t b, int64_t s, int64_t h, int64_t d, int64_t n_cand);
+
+/*
+ * dsa_indexer_score_topk with a caller-provided device workspace (16-byte aligned,
+ * workspace_bytes as given by dsa_indexer_workspace_bytes). Same results. For
+ * h == 64, d == 128 the scores go to the workspace and a second kernel ranks each
+ * token's row (faster than the single kernel, which keeps four tokens' keys in LDS);
+ * with a smaller or NULL workspace it behaves as dsa_indexer_score_topk. The
+ * workspace content is scratch: not read before it is written, not needed afterwards.
+ * Replaces the same reference call as dsa_indexer_score_topk (task2_v0_ref.py:131-143).
+ */
+int dsa_indexer_score_topk_ws(const void* q, const void* kv_cache, int64_t kv_batch_stride,
+                              const void* wl, float w_scale, const void* freqs_cis,
+                              int32_t rope_mode, int64_t* out, int64_t b, int64_t s,
+                              int64_t h, int64_t d, int64_t rd, int64_t n_cand, int64_t k_out,
+                              int64_t ratio, int32_t causal, int64_t offset, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
+/*
  * Task2 score stage alone: writes the bf16 index_score [b, s, n_cand] that the reference
  * hands to topk (reference/task2_v0_ref.py:131-137), with masked entries = -inf in the
  * causal case. Same arguments and requirements as dsa_indexer_score_topk; `scores` is a

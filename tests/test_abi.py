@@ -12,7 +12,7 @@ from ascendc_kernel_amd import _native
 
 def _declared():
     text = open(os.path.join(REPO, "include", "dsa_abi.h")).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(dsa_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(dsa_\w+)\s*\(", text, re.M)))
 
 
 def test_library_present_and_loads():

@@ -144,3 +144,25 @@ def test_full_shape_c5_indexer(gpu):
         want = r(x, qr, sp, off)
         torch.cuda.synchronize()
     _check_equal(got, want, "c5-indexer")
+
+
+@pytest.mark.parametrize("seqlen,topk,start_pos", [(1024, 2048, 0), (700, 300, 0), (96, 64, 160)])
+def test_wide_single_kernel_and_workspace_paths(gpu, seqlen, topk, start_pos):
+    """dsa_indexer_score_topk (keys of 4 tokens in LDS, fused top-k) and
+    dsa_indexer_score_topk_ws (keys in the workspace, per-token select kernel) give the
+    reference's indices."""
+    end = start_pos + seqlen
+    args = _args(end, topk)
+    m, r = _pair(args, 300 + seqlen, end, 1, gpu, wstd=0.02)
+    g = torch.Generator().manual_seed(seqlen + 7)
+    x = torch.randn(1, seqlen, 7168, generator=g).to(torch.bfloat16).to(gpu)
+    qr = torch.randn(1, seqlen, 1536, generator=g).to(torch.bfloat16).to(gpu)
+    _say("wide paths", seqlen, topk, start_pos)
+    want = r(x, qr, start_pos, 3)
+    q = torch.nn.functional.linear(qr, m.wq_b.weight).unflatten(-1, (64, 128)).contiguous()
+    wl = torch.nn.functional.linear(x, m.weights_proj.weight)
+    k = min(topk, end)
+    for ws in (False, True):
+        got = _native.indexer_score_topk(q, m.kv_cache, wl, 128 ** -0.5 * 64 ** -0.5, m.freqs_cis[start_pos:end],
+                                         64, end, k, 1, start_pos == 0, 3, use_workspace=ws)
+        _check_equal(got, want, f"wide-ws{ws}-{seqlen}-{topk}")
