@@ -25,8 +25,9 @@
 // does the exact products and the fp32 additions), one v_permlane32_swap joins
 // the lane halves, and the even/odd totals meet in LDS. Scores become 16-bit
 // order keys in LDS; per token a two-pass 8-bit radix select finds the k-th key,
-// the picks are compacted ([> k-th] then [== k-th] in index order) and
-// bitonic-sorted on (key, ~index) before the int64 indices are written.
+// the picks are compacted ([> k-th] then [== k-th] in index order) and put in
+// (key descending, index ascending) order by a stable two-pass LSD radix sort
+// before the int64 indices are written.
 #include "dsa_common.h"
 
 using namespace dsa;
@@ -61,7 +62,7 @@ struct WideParams {
   int64_t offset;
   int32_t groups;       // ceil(S / kTok)
   int32_t tpad;         // key row length in LDS (T rounded up to 32)
-  int32_t psort;        // power of two >= K (bitonic size)
+  int32_t psort;        // power of two >= K (pick buffer length)
 };
 
 template <int N>
@@ -155,18 +156,108 @@ __device__ __forceinline__ void hist_add_grouped(uint32_t* hist, uint32_t bin, b
   }
 }
 
+// Stable sort, descending on the 8-bit digit (v >> sh) & 255, of the n values
+// src[0..n) into dst, by the NW waves (thread index tt) of a workgroup whose every
+// thread calls this. Wave w takes the w-th contiguous chunk in rounds of 64; per
+// round the lanes holding the same digit are found with one ballot per digit bit
+// that varies in the round, which gives each value its rank among equal digits
+// of the chunk so far (a per-wave running count per digit in wr). The digit
+// totals of all waves then give every (wave, digit) its output start.
+// wr: NW * 256 words, wt: NW words of LDS.
+template <int NW>
+__device__ void radix_pass_desc(const uint32_t* src, uint32_t* dst, int n, int sh, uint32_t* wr,
+                                uint32_t* wt, int tt) {
+  constexpr int kR = kMaxK / (64 * NW);  // rounds per wave at most
+  const int lane = tt & 63, wv = tt >> 6;
+  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+  const int chunk = ((n + NW - 1) / NW + 63) & ~63;
+  const int c_beg = wv * chunk;
+  const int c_end = min(n, c_beg + chunk);
+  for (int i = tt; i < NW * 256; i += 64 * NW) wr[i] = 0u;
+  __syncthreads();
+  uint32_t* myw = wr + wv * 256;
+  uint32_t vals[kR], rk[kR];
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    const int c = c_beg + 64 * r + lane;
+    const bool act = c < c_end;
+    const uint32_t v = act ? src[c] : 0u;
+    const uint32_t d = 255u - ((v >> sh) & 255u);
+    const uint64_t am = __ballot(act);
+    uint64_t m = am;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (d >> b) & 1u;
+      const uint64_t bb = __ballot(act && bit);
+      if (bb != 0ull && bb != am) m &= bit ? bb : ~bb;  // uniform test: the bit varies
+    }
+    const uint32_t rank = (uint32_t)__builtin_popcountll(m & below);
+    uint32_t old = 0u;
+    if (act) old = myw[d];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (act && rank == 0u) myw[d] = old + (uint32_t)__builtin_popcountll(m);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    vals[r] = v;
+    rk[r] = old + rank;
+  }
+  __syncthreads();
+  // Exclusive scan of the digit totals (digit order = output order), then the
+  // start of every (wave, digit) block, written over the counts.
+  constexpr int kQ = 256 / (64 * NW);  // digits per thread
+  uint32_t cnt[kQ][NW];
+  uint32_t loc = 0u;
+#pragma unroll
+  for (int i = 0; i < kQ; ++i)
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      cnt[i][w] = wr[w * 256 + kQ * tt + i];
+      loc += cnt[i][w];
+    }
+  uint32_t incl = loc;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wt[wv] = incl;
+  __syncthreads();
+  uint32_t run = incl - loc;
+  for (int w = 0; w < wv; ++w) run += wt[w];
+#pragma unroll
+  for (int i = 0; i < kQ; ++i)
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      wr[w * 256 + kQ * tt + i] = run;
+      run += cnt[i][w];
+    }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    const int c = c_beg + 64 * r + lane;
+    if (c < c_end) {
+      const uint32_t d = 255u - ((vals[r] >> sh) & 255u);
+      dst[myw[d] + rk[r]] = vals[r];
+    }
+  }
+  __syncthreads();
+}
+
 // Top-K of one row of 16-bit order keys held in LDS (keys[0..nv) are the valid
-// candidates), by `nthr` threads (thread index tt, waves of 64) of a workgroup
-// whose every thread calls this (it contains __syncthreads): two-pass 8-bit radix
-// select of the K-th key, compaction of the picks ([keys > k-th] then the first
-// [== k-th] in index order), bitonic sort of (key, ~index) composites descending,
-// int64 output (index + offset; -1 for picks beyond the valid candidates).
-// hist: 512 words, sel: 4 words, sb: psort words of LDS.
-__device__ void select_topk_row(const uint16_t* keys, int nv, int K, int psort, uint32_t* hist,
-                                int32_t* sel, uint32_t* sb, int tt, int nthr, int64_t* out_row,
-                                int64_t offset) {
+// candidates), by the NW waves (thread index tt) of a workgroup whose every thread
+// calls this (it contains __syncthreads): two-pass 8-bit radix select of the K-th
+// key, compaction of the picks ([keys > k-th] then the first [== k-th], each in
+// index order) as (key << 16 | ~index) composites, a stable radix sort of the
+// picks on the key, descending (equal keys keep index order), and the int64
+// output (index + offset; -1 for picks beyond the valid candidates).
+// hist: max(512, NW * 256) words, sel: 4 words, sb and tmp: K words of LDS each.
+template <int NW>
+__device__ void select_topk_row(const uint16_t* keys, int nv, int K, uint32_t* hist, int32_t* sel,
+                                uint32_t* sb, uint32_t* tmp, int tt, int64_t* out_row, int64_t offset) {
+  constexpr int nthr = 64 * NW;
   const int lane = tt & 63;
-  const int nw = nthr >> 6, wv = tt >> 6;
+  const int nw = NW, wv = tt >> 6;
   const bool selecting = nv > K;
   uint32_t* h1 = hist;
   uint32_t* h2 = hist + 256;
@@ -253,45 +344,10 @@ __device__ void select_topk_row(const uint16_t* keys, int nv, int K, int psort, 
   } else {
     for (int c = tt; c < nv; c += nthr) sb[c] = ((uint32_t)keys[c] << 16) | (0xffffu - (uint32_t)c);
   }
-  for (int j = count + tt; j < psort; j += nthr) sb[j] = 0u;  // sorts last
   __syncthreads();
-  // Bitonic sort, descending. Wave wv owns elements [wv * seg, (wv + 1) * seg); the
-  // steps whose pairs stay inside a segment (stride < seg) run with wave-level
-  // ordering only, the others between workgroup barriers.
-  const int seg = psort / nw;
-  for (int size = 2; size <= psort; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const bool cross = stride >= seg || seg < 128;
-      if (cross) {
-        __syncthreads();
-        for (int i = tt; i < (psort >> 1); i += nthr) {
-          const int lo = 2 * i - (i & (stride - 1));
-          const int hi = lo + stride;
-          const bool desc = (lo & size) == 0;
-          const uint32_t x = sb[lo], z = sb[hi];
-          if ((x < z) == desc) {
-            sb[lo] = z;
-            sb[hi] = x;
-          }
-        }
-        __syncthreads();
-      } else {
-        for (int i = wv * (seg >> 1) + lane; i < (wv + 1) * (seg >> 1); i += 64) {
-          const int lo = 2 * i - (i & (stride - 1));
-          const int hi = lo + stride;
-          const bool desc = (lo & size) == 0;
-          const uint32_t x = sb[lo], z = sb[hi];
-          if ((x < z) == desc) {
-            sb[lo] = z;
-            sb[hi] = x;
-          }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-  }
-  __syncthreads();
+  // Stable LSD radix sort on the key: low byte, then high byte.
+  radix_pass_desc<NW>(sb, tmp, count, 16, hist, reinterpret_cast<uint32_t*>(sel), tt);
+  radix_pass_desc<NW>(tmp, sb, count, 24, hist, reinterpret_cast<uint32_t*>(sel), tt);
   if (out_row != nullptr)
     for (int j = tt; j < K; j += nthr) {
       const uint32_t comp = sb[j];
@@ -300,6 +356,11 @@ __device__ void select_topk_row(const uint16_t* keys, int nv, int K, int psort, 
     }
 }
 
+// kFused: the keys of the 4 tokens stay in LDS and each token's two waves run
+// the top-k (select_topk_row) at the end. Otherwise the per-candidate results go
+// to p.gkeys and the kernel ends after the scores; that instantiation carries no
+// select code, which keeps its register count low enough for two workgroups per CU.
+template <bool kFused>
 __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* keys = reinterpret_cast<uint16_t*>(smem);                                   // [kTok][tpad]
@@ -308,6 +369,7 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
   uint32_t* hist = reinterpret_cast<uint32_t*>(xbuf + 2 * kTok * kTileC);             // [kTok][2][256]
   int32_t* sel = reinterpret_cast<int32_t*>(hist + kTok * 512);                       // [kTok][4]
   uint32_t* sortbuf = reinterpret_cast<uint32_t*>(ring);  // [kTok][psort], after the scores
+  uint32_t* tmpbuf = reinterpret_cast<uint32_t*>(sel + kTok * 4);                     // [kTok][psort]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -408,12 +470,22 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
       const int c = kTileC * n + col;
       if (c < nv) {
         const uint16_t v = (uint16_t)(p.graw ? sc : order_key16(sc));
-        if (gdst != nullptr) gdst[c] = v;
-        else mykeys[c] = v;
+        if constexpr (kFused) mykeys[c] = v;
+        else if (gdst != nullptr) gdst[c] = v;
       }
     }
   };
 
+  auto qk = [&](int n) {
+    const u32x4* kt = ring + (n % kRingW) * 512;
+    f32x16 acc = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8 bk = __builtin_bit_cast(bf16x8, kt[swz(col, 2 * ks + hf)]);
+      acc = mfma32x32x16(qa[ks], bk, acc);
+    }
+    return acc;
+  };
   for (int n = 0; n < ntiles; ++n) {
     if (n + 2 < ntiles) wait_vmcnt<2>();
     else if (n + 1 < ntiles) wait_vmcnt<1>();
@@ -421,14 +493,7 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     __syncthreads();  // tile n is in LDS; tile n-1's buffer and odd totals are consumed/visible
     if (n > 0) finalize(n - 1);
     if (n + kRingW - 1 < ntiles) issue(n + kRingW - 1);
-
-    const u32x4* kt = ring + (n % kRingW) * 512;
-    f32x16 s = {};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 bk = __builtin_bit_cast(bf16x8, kt[swz(col, 2 * ks + hf)]);
-      s = mfma32x32x16(qa[ks], bk, s);
-    }
+    const f32x16 s = qk(n);
     float acc_a = 0.f, acc_b = 0.f;
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
@@ -456,19 +521,25 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
   __syncthreads();
 
   const int tt = y * 64 + lane;  // thread of the token (0..127)
-  if (p.gkeys != nullptr) {
+  if constexpr (!kFused) {
     if (p.graw && gdst != nullptr)  // score dump: never-valid candidates are -inf
       for (int c = nv + tt; c < p.T; c += 128) gdst[c] = (uint16_t)0xff80u;
-    return;
+  } else {
+    select_topk_row<2>(mykeys, nv, p.K, hist + tl * 512, sel + tl * 4, sortbuf + tl * p.psort,
+                       tmpbuf + tl * p.psort, tt, tok_ok ? p.out + row_bt * p.K : nullptr, p.offset);
   }
-
-  select_topk_row(mykeys, nv, p.K, p.psort, hist + tl * 512, sel + tl * 4, sortbuf + tl * p.psort, tt, 128,
-                  tok_ok ? p.out + row_bt * p.K : nullptr, p.offset);
 }
 
 
 // Top-K of rows of 16-bit order keys written by ix_wide_kernel: one workgroup
-// (256 threads) per token row.
+// (256 threads) per token row. Thread tt holds keys [32 tt, 32 tt + 32) of the row
+// in registers (index order = thread order, then register order):
+//   1. high-byte histogram (LDS atomics), the bin of the K-th key; low-byte
+//      histogram of that bin, the K-th key itself (kth) and n_gt = #(keys > kth);
+//   2. one workgroup scan of the per-thread counts (#(> kth) | #(== kth) << 16)
+//      places every pick: [> kth] at [0, n_gt) and the first K - n_gt [== kth]
+//      after them, each in index order;
+//   3. stable two-pass radix sort of the picks on the key (descending), int64 out.
 struct SelParams {
   const uint16_t* keys;  // [B*S, T]
   int64_t* out;          // [B*S, K]
@@ -478,10 +549,13 @@ struct SelParams {
 
 __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
   extern __shared__ __align__(16) uint8_t smem[];
-  uint32_t* sortbuf = reinterpret_cast<uint32_t*>(smem);   // [psort]
-  uint32_t* hist = sortbuf + p.psort;                       // [512]
-  int32_t* sel = reinterpret_cast<int32_t*>(hist + 512);    // [4]
-  uint16_t* keys = reinterpret_cast<uint16_t*>(sel + 4);    // [T] (8-byte aligned)
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem);     // [1024]: h1 | h2, then radix counts
+  uint32_t* wt = hist + 1024;                              // [4] wave totals
+  int32_t* sel = reinterpret_cast<int32_t*>(wt + 4);      // [4]
+  uint32_t* sortbuf = reinterpret_cast<uint32_t*>(sel + 4);  // [psort]
+  uint32_t* tmpbuf = sortbuf + p.psort;                    // [psort]
+  const int tt = threadIdx.x;
+  const int lane = tt & 63, wv = tt >> 6;
   const int64_t row = blockIdx.x;
   const int t = (int)(row % p.S);
   int nv = p.T;
@@ -489,25 +563,107 @@ __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
     nv = (t + 1) / p.ratio;
     if (nv > p.T) nv = p.T;
   }
-  // The row in 8-byte pieces (T % 4 == 0), all loads of a thread issued before its
-  // stores: T <= 8192 keys = at most 8 pieces per thread.
-  const uint2* src = reinterpret_cast<const uint2*>(p.keys + row * p.T);
-  uint2* dst = reinterpret_cast<uint2*>(keys);
-  const int nq = (nv + 3) >> 2;
-  uint2 v[8];
+  const int K = p.K;
+  const bool selecting = nv > K;
+  // Keys of this thread (8-byte loads: rows are 8-byte aligned since T % 4 == 0).
+  const uint2* src = reinterpret_cast<const uint2*>(p.keys + row * p.T) + 8 * tt;
+  const int c0 = 32 * tt;
+  // Order keys are >= 0x007f (-inf), so 0 marks the positions past nv.
+  uint2 kw[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = (int)threadIdx.x + 256 * j;
-    v[j] = i < nq ? src[i] : uint2{0u, 0u};
+  for (int i = 0; i < 8; ++i) {
+    const int rem = nv - (c0 + 4 * i);  // valid keys in this piece
+    kw[i] = rem > 0 ? src[i] : uint2{0u, 0u};
+    if (rem == 1) kw[i] = uint2{kw[i].x & 0xffffu, 0u};
+    if (rem == 2) kw[i].y = 0u;
+    if (rem == 3) kw[i].y &= 0xffffu;
   }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = (int)threadIdx.x + 256 * j;
-    if (i < nq) dst[i] = v[j];
-  }
+  auto key_of = [&](int e) -> uint32_t {
+    const uint32_t w = (e & 2) ? kw[e >> 2].y : kw[e >> 2].x;
+    return (e & 1) ? (w >> 16) : (w & 0xffffu);
+  };
+  for (int i = tt; i < 512; i += 256) hist[i] = 0u;
   __syncthreads();
-  select_topk_row(keys, nv, p.K, p.psort, hist, sel, sortbuf, threadIdx.x, 256, p.out + row * p.K,
-                  p.offset);
+  uint32_t kth = 0u, n_gt = (uint32_t)nv, need_eq = 0u;
+  if (selecting) {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const uint32_t u = key_of(e);
+      if (u != 0u) atomicAdd(&hist[u >> 8], 1u);
+    }
+    __syncthreads();
+    if (wv == 0) {
+      uint32_t gt;
+      const int b1 = find_bin64(hist, lane, (uint32_t)K, gt);
+      if (lane == 0) {
+        sel[0] = b1;
+        sel[1] = (int32_t)gt;
+      }
+    }
+    __syncthreads();
+    const uint32_t b1 = (uint32_t)sel[0];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const uint32_t u = key_of(e);
+      if (u != 0u && (u >> 8) == b1) atomicAdd(&hist[256 + (u & 255u)], 1u);
+    }
+    __syncthreads();
+    if (wv == 0) {
+      uint32_t gt;
+      const uint32_t above = (uint32_t)sel[1];
+      const int b0 = find_bin64(hist + 256, lane, (uint32_t)K - above, gt);
+      if (lane == 0) {
+        sel[2] = b0;
+        sel[3] = (int32_t)(above + gt);
+      }
+    }
+    __syncthreads();
+    kth = (b1 << 8) | (uint32_t)sel[2];
+    n_gt = (uint32_t)sel[3];
+    need_eq = (uint32_t)K - n_gt;
+  }
+  // Per-thread pick counts, packed (> kth) | (== kth) << 16, and their exclusive
+  // scan over the workgroup.
+  // Without selection every key > 0 is a pick; kth >= 0x007f when selecting, so
+  // the 0 marks never count.
+  const uint32_t kth_e = selecting ? kth : 0xffffffffu;
+  uint32_t cnt = 0u;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const uint32_t u = key_of(e);
+    cnt += (u > kth ? 1u : 0u) + (u == kth_e ? 0x10000u : 0u);
+  }
+  uint32_t incl = cnt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wt[wv] = incl;
+  __syncthreads();
+  uint32_t base = incl - cnt;
+  for (int w = 0; w < wv; ++w) base += wt[w];
+  uint32_t og = base & 0xffffu, oe = base >> 16;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const uint32_t u = key_of(e);
+    const uint32_t comp = (u << 16) | (0xffffu - (uint32_t)(c0 + e));
+    if (u > kth) {
+      sortbuf[og++] = comp;
+    } else if (u == kth_e) {
+      if (oe < need_eq) sortbuf[n_gt + oe] = comp;
+      ++oe;
+    }
+  }
+  const int count = selecting ? K : nv;
+  __syncthreads();
+  radix_pass_desc<4>(sortbuf, tmpbuf, count, 16, hist, wt, tt);
+  radix_pass_desc<4>(tmpbuf, sortbuf, count, 24, hist, wt, tt);
+  int64_t* out_row = p.out + row * K;
+  for (int j = tt; j < K; j += 256) {
+    const uint32_t comp = sortbuf[j];
+    out_row[j] = (j < count) ? (int64_t)(0xffffu - (comp & 0xffffu)) + p.offset : (int64_t)-1;
+  }
 }
 
 }  // namespace
@@ -565,15 +721,19 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
   } else {
     p.tpad = (int32_t)((n_cand + kTileC - 1) / kTileC * kTileC);
     smem = (size_t)kTok * p.tpad * 2 + (size_t)kRingW * 8192 + 2 * kTok * kTileC * 4 +
-           kTok * 512 * 4 + kTok * 4 * 4;
+           kTok * 512 * 4 + kTok * 4 * 4 + (size_t)kTok * ps * 4;
   }
   if (smem > 160 * 1024) return DSA_ERR_UNSUPPORTED;
-  if (hipFuncSetAttribute((const void*)ix_wide_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)smem) != hipSuccess)
+  const bool fused = p.gkeys == nullptr;
+  const void* kfn = fused ? (const void*)ix_wide_kernel<true> : (const void*)ix_wide_kernel<false>;
+  if (hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
     return DSA_ERR_LAUNCH;
   const int64_t blocks = b * p.groups;
   if (blocks > INT32_MAX || b * s > INT32_MAX) return DSA_ERR_SHAPE;
-  hipLaunchKernelGGL(ix_wide_kernel, dim3((unsigned)blocks), dim3(512), smem, stream, p);
+  if (fused)
+    hipLaunchKernelGGL(ix_wide_kernel<true>, dim3((unsigned)blocks), dim3(512), smem, stream, p);
+  else
+    hipLaunchKernelGGL(ix_wide_kernel<false>, dim3((unsigned)blocks), dim3(512), smem, stream, p);
   if (hipGetLastError() != hipSuccess) return DSA_ERR_LAUNCH;
   if (two_pass) {
     SelParams sp;
@@ -586,7 +746,7 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
     sp.causal = p.causal;
     sp.psort = p.psort;
     sp.offset = offset;
-    const size_t smem2 = (size_t)ps * 4 + 512 * 4 + 16 + (size_t)((n_cand + 7) / 8 * 8) * 2;
+    const size_t smem2 = 1024 * 4 + 16 + 16 + (size_t)ps * 8;
     if (hipFuncSetAttribute((const void*)ix_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)smem2) != hipSuccess)
       return DSA_ERR_LAUNCH;
