@@ -92,6 +92,7 @@ __device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t voff, uint32_t m0
 
 __device__ __forceinline__ int swz(int r, int c) { return r * 16 + (c ^ (r & 15)); }
 
+
 // Head of MFMA row R in the wave for head parity y: lane half hf = (R/4)%2 and
 // register r = 4(R/8) + R%4 hold head y + 4hf + 2(r%2) + 8(r/2), so a lane has
 // accumulators 2hf and 2hf+1 (heads y + 2i + 8m) for m = 0..7 in registers
@@ -476,24 +477,26 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     }
   };
 
-  auto qk = [&](int n) {
-    const u32x4* kt = ring + (n % kRingW) * 512;
-    f32x16 acc = {};
+  // Tiles in groups of kRingW, so that the ring slot (and with it every LDS
+  // operand address) is a compile-time offset from loop-invariant lane addresses.
+  for (int n0 = 0; n0 < ntiles; n0 += kRingW) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 bk = __builtin_bit_cast(bf16x8, kt[swz(col, 2 * ks + hf)]);
-      acc = mfma32x32x16(qa[ks], bk, acc);
-    }
-    return acc;
-  };
-  for (int n = 0; n < ntiles; ++n) {
+   for (int j = 0; j < kRingW; ++j) {
+    const int n = n0 + j;
+    if (n >= ntiles) break;
     if (n + 2 < ntiles) wait_vmcnt<2>();
     else if (n + 1 < ntiles) wait_vmcnt<1>();
     else wait_vmcnt<0>();
     __syncthreads();  // tile n is in LDS; tile n-1's buffer and odd totals are consumed/visible
     if (n > 0) finalize(n - 1);
     if (n + kRingW - 1 < ntiles) issue(n + kRingW - 1);
-    const f32x16 s = qk(n);
+    const u32x4* kt = ring + j * 512;
+    f32x16 s = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8 bk = __builtin_bit_cast(bf16x8, kt[swz(col, 2 * ks + hf)]);
+      s = mfma32x32x16(qa[ks], bk, s);
+    }
     float acc_a = 0.f, acc_b = 0.f;
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
@@ -515,6 +518,7 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     } else {
       t0val = ty;
     }
+   }
   }
   __syncthreads();
   if (ntiles > 0) finalize(ntiles - 1);
