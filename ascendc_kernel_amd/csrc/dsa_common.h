@@ -48,6 +48,50 @@ __device__ __forceinline__ void st_nt(T* p, T v) {
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource (V#) of a raw byte range: base, stride 0, num_records =
+// bytes (accesses at or beyond it read as zero, stores there are dropped),
+// word3 = the gfx9 raw-buffer format word. The base is made wave-uniform.
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return i32x4{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a),
+               __builtin_amdgcn_readfirstlane((int32_t)((a >> 32) & 0xffffu)),
+               (int32_t)bytes, 0x00020000};
+}
+
+// The same range as a typed resource for the compiler's buffer intrinsics
+// (__builtin_amdgcn_raw_buffer_load_b128 / _store_b128).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)(((uint64_t)hi << 32) | lo), 0,
+                                           (int)bytes, 0x00020000);
+}
+
+// One buffer_load_dwordx4 ... lds: lane l copies the 16 B at byte offset voff of
+// the resource to LDS byte address m0 + 16 * l (m0 is wave-uniform). It is
+// issued from inline asm so that the compiler does not track it: its own
+// waitcnt insertion would otherwise put a vmcnt(0) in front of every LDS read
+// of the ring. The kernel waits for these copies itself (wait_vmcnt + barrier).
+// M0 is an input operand (the compiler sets it); the s_nop covers the
+// M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t voff, uint32_t m0) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "{m0}"(m0)
+               : "memory");
+}
+
 // One complex product of RoPE in the rounding torch uses.
 //  DSA_ROPE_CPU: vectorised CPU kernel, every product rounded, no FMA.
 //  DSA_ROPE_TORCH_ROCM: the broadcast elementwise kernel of torch-ROCm; its

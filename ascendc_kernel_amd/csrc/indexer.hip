@@ -31,6 +31,8 @@ using namespace dsa;
 
 namespace {
 
+typedef short s16v2 __attribute__((ext_vector_type(2)));
+
 constexpr int kH = 16;  // index heads handled by the fused kernel
 constexpr int kD = 64;  // index head dim handled by the fused kernel
 
@@ -150,22 +152,40 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   const int ntile = (nv_max + 31) >> 5;
   const int ntile_all = (p.keys_bytes / 128);
 
-  // Head weights of this half's token, bf16(fp32(wl) * w_scale), fp32 copies.
-  float w[kH];
-  if (t < p.S) {
-    const u32x4* wp = reinterpret_cast<const u32x4*>(p.wl + ((int64_t)b * p.S + t) * kH);
-    const u32x4 w0 = wp[0], w1 = wp[1];
+  // Head weights of this half's token, bf16(fp32(wl) * w_scale), as v_dot2
+  // operands for the products of word k of the swapped scores (slots 2k, 2k+1):
+  // wlo[k] = (w(head of slot 2k), 0), whi[k] = (0, w(head of slot 2k+1)).
+  uint32_t wlo[8], whi[8];
+  {
+    uint32_t wb[kH];
+    if (t < p.S) {
+      const u32x4* wp = reinterpret_cast<const u32x4*>(p.wl + ((int64_t)b * p.S + t) * kH);
+      const u32x4 w0 = wp[0], w1 = wp[1];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      w[2 * i] = bf2f(f2bf(bf_lo(w0[i]) * p.wscale));
-      w[2 * i + 1] = bf2f(f2bf(bf_hi(w0[i]) * p.wscale));
-      w[8 + 2 * i] = bf2f(f2bf(bf_lo(w1[i]) * p.wscale));
-      w[8 + 2 * i + 1] = bf2f(f2bf(bf_hi(w1[i]) * p.wscale));
+      for (int i = 0; i < 4; ++i) {
+        wb[2 * i] = f2bf(bf_lo(w0[i]) * p.wscale);
+        wb[2 * i + 1] = f2bf(bf_hi(w0[i]) * p.wscale);
+        wb[8 + 2 * i] = f2bf(bf_lo(w1[i]) * p.wscale);
+        wb[8 + 2 * i + 1] = f2bf(bf_hi(w1[i]) * p.wscale);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kH; ++i) wb[i] = 0u;
     }
-  } else {
 #pragma unroll
-    for (int i = 0; i < kH; ++i) w[i] = 0.f;
+    for (int k = 0; k < 8; ++k) {
+      const int r = 2 * k;
+      const int h0 = (r < 4) ? r : (r < 8) ? r + 4 : (r < 12) ? r - 4 : r;
+      wlo[k] = wb[h0];
+      whi[k] = wb[h0 + 1] << 16;
+    }
   }
+  // bf16 pairs (1, 0) and (0, 1) kept in SGPRs: as literals the compiler would
+  // encode (1, 0) as the inline constant 1.0, which v_dot2c reads as fp32 bits.
+  uint32_t one_lo_bits = 0x00003f80u, one_hi_bits = 0x3f800000u;
+  asm volatile("" : "+s"(one_lo_bits), "+s"(one_hi_bits));
+  const bf16v2 one_lo = __builtin_bit_cast(bf16v2, one_lo_bits);
+  const bf16v2 one_hi = __builtin_bit_cast(bf16v2, one_hi_bits);
 
   // A operand: row i = lane % 32 is (token t0 + i/16, head i%16); lane holds
   // channels 16ks + 8(lane/32) .. +7 of that row, RoPE applied when asked.
@@ -209,30 +229,36 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   *reinterpret_cast<u32x4*>(myhist + 8 * hl + 4) = u32x4{0u, 0u, 0u, 0u};
   lds_fence();
 
-  const uint16_t* kvb = p.kv + (int64_t)b * p.kvbs;
+  // Candidate rows through a buffer resource: rows >= T read as zero. The next
+  // tile's operands are requested before the current tile is processed.
+  const __amdgpu_buffer_rsrc_t krs = buf_rsrc(p.kv + (int64_t)b * p.kvbs, (uint32_t)p.T * kD * 2);
   const int kcol = lane & 31;
   const int khalf = lane >> 5;
-  for (int tile = 0; tile < ntile; ++tile) {
+  auto load_kb = [&](int tile, bf16x8* kb) {
     // B operand: candidate 32*tile + lane%32, channels 16ks + 8(lane/32) .. +7.
-    const int cand = 32 * tile + kcol;
-    bf16x8 kb[4];
-    if (cand < p.T) {
-      const uint16_t* src = kvb + (int64_t)cand * kD + 8 * khalf;
+    const int off = ((32 * tile + kcol) * kD + 8 * khalf) * 2;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        kb[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(src + 16 * ks));
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kb[ks] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-    }
+    for (int ks = 0; ks < 4; ++ks)
+      kb[ks] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 32 * ks, 0, 0));
+  };
+  bf16x8 kb[4], kn[4];
+  load_kb(0, kb);
+  for (int tile = 0; tile < ntile; ++tile) {
+    load_kb(tile + 1, kn);
     f32x16 acc = {};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc = mfma32x32x16(qa[ks], kb[ks], acc);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kb[ks] = kn[ks];
 
-    // relu + the einsum's bf16 rounding, two heads per word: word k holds slots 2k, 2k+1.
+    // The einsum's bf16 rounding, then relu on the bf16 bit patterns (both heads
+    // of a word at once): word k holds slots 2k, 2k+1.
     uint32_t pk[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) pk[k] = pack_bf2(fmaxf(acc[2 * k], 0.f), fmaxf(acc[2 * k + 1], 0.f));
+    for (int k = 0; k < 8; ++k) {
+      s16v2 h = __builtin_bit_cast(s16v2, pack_bf2(acc[2 * k], acc[2 * k + 1]));
+      pk[k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(h, (s16v2){0, 0}));
+    }
     // Exchange halves: afterwards lanes 0..31 hold token t0, lanes 32..63 token
     // t0+1, all 16 heads of candidate 32*tile + lane%32. Slot r holds head
     // r (r<4), r+4 (4<=r<8), r-4 (8<=r<12), r (12<=r). (The swap operands are
@@ -243,20 +269,26 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
       pk[k] = (uint32_t)sw[0];
       pk[k + 4] = (uint32_t)sw[1];
     }
-    // * w -> bf16, as fp32 values.
-    float v[16];
+    // * w, rounded to bf16 (the products are exact in fp32).
+    bf16v2 pb[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int r = 2 * k;
-      const int h0 = (r < 4) ? r : (r < 8) ? r + 4 : (r < 12) ? r - 4 : r;
-      const uint32_t pb = pack_bf2(bf_lo(pk[k]) * w[h0], bf_hi(pk[k]) * w[h0 + 1]);
-      v[r] = bf_lo(pb);
-      v[r + 1] = bf_hi(pb);
+      const bf16v2 pv = __builtin_bit_cast(bf16v2, pk[k]);
+      const float p0 = __builtin_amdgcn_fdot2_f32_bf16(pv, __builtin_bit_cast(bf16v2, wlo[k]), 0.0f, false);
+      const float p1 = __builtin_amdgcn_fdot2_f32_bf16(pv, __builtin_bit_cast(bf16v2, whi[k]), 0.0f, false);
+      pb[k] = __builtin_bit_cast(bf16v2, pack_bf2(p0, p1));
     }
-    // Head j is in slot j (j<4), j+4 -> slot j+8, j+8 -> slot j+4, j+12 -> slot j+12.
+    // Accumulator j takes heads j, j+4, j+8, j+12 = slots j, j+8, j+4, j+12, all
+    // in half j%2 of words j/2 + {0, 4, 2, 6}; each v_dot2c adds one product.
     float a4[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a4[j] = (((0.0f + v[j]) + v[j + 8]) + v[j + 4]) + v[j + 12];
+    for (int j = 0; j < 4; ++j) {
+      const bf16v2 sel = (j & 1) ? one_hi : one_lo;
+      float a = __builtin_amdgcn_fdot2_f32_bf16(pb[j >> 1], sel, 0.0f, false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(pb[(j >> 1) + 4], sel, a, false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(pb[(j >> 1) + 2], sel, a, false);
+      a4[j] = __builtin_amdgcn_fdot2_f32_bf16(pb[(j >> 1) + 6], sel, a, false);
+    }
     const float tot = ((a4[0] + a4[1]) + a4[2]) + a4[3];
     uint16_t sc = f2bf(tot);
     const int c = 32 * tile + hl;

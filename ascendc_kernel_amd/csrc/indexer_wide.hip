@@ -42,7 +42,6 @@ constexpr int kRingW = 4;    // LDS tile buffers
 constexpr int kMaxT = 8192;
 constexpr int kMaxK = 2048;
 
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef short s16v2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
@@ -65,30 +64,8 @@ struct WideParams {
   int32_t psort;        // power of two >= K (pick buffer length)
 };
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
-// Raw buffer resource: base, stride 0, num_records = bytes (reads at or beyond
-// read zero), gfx9 raw-buffer format word.
-__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)(uintptr_t)base;
-  return i32x4{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a),
-               __builtin_amdgcn_readfirstlane((int32_t)((a >> 32) & 0xffffu)), (int32_t)bytes,
-               0x00020000};
-}
 
-// buffer_load_dwordx4 ... lds: lane l copies 16 B at byte offset voff to LDS
-// address m0 + 16 l. From inline asm so that the compiler does not track it
-// (it would put a vmcnt(0) before every LDS read); waited with wait_vmcnt.
-__device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t voff, uint32_t m0) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(rsrc), "{m0}"(m0)
-               : "memory");
-}
 
 __device__ __forceinline__ int swz(int r, int c) { return r * 16 + (c ^ (r & 15)); }
 

@@ -50,39 +50,6 @@ struct GatherParams {
   float scale_log2;      // softmax_scale * log2(e)
 };
 
-// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
-// vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-
-// Buffer resource (V#) of a raw byte range: base, stride 0, num_records =
-// bytes (accesses at or beyond it read as zero), word3 = the gfx9 raw-buffer
-// format word.
-__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)(uintptr_t)base;
-  return i32x4{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a),
-               __builtin_amdgcn_readfirstlane((int32_t)((a >> 32) & 0xffffu)),
-               (int32_t)bytes, 0x00020000};
-}
-
-// One buffer_load_dwordx4 ... lds: lane l copies the 16 B at byte offset voff of
-// the resource to LDS byte address m0 + 16 * l (m0 is wave-uniform). It is
-// issued from inline asm so that the compiler does not track it: its own
-// waitcnt insertion would otherwise put a vmcnt(0) in front of every LDS read
-// of the ring. The kernel waits for these copies itself (wait_vmcnt + barrier).
-// M0 is an input operand (the compiler sets it); the s_nop covers the
-// M0-write -> LDS-DMA hazard.
-__device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t voff, uint32_t m0) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(rsrc), "{m0}"(m0)
-               : "memory");
-}
 
 // Output channel of row i of d-tile dt (O^T rows): lane half hf = (i >> 2) & 1
 // gets the contiguous channels 64*hf .. 64*hf + 63 across the four d-tiles.

@@ -40,7 +40,6 @@ constexpr uint32_t kOob = 0xfffffff0u;          // a copy offset beyond any reso
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 struct MlaParams {
   const uint16_t* q;     // [B, M, H, 576]
@@ -53,27 +52,8 @@ struct MlaParams {
   float scale_log2;
 };
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
-__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)(uintptr_t)base;
-  return i32x4{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a),
-               __builtin_amdgcn_readfirstlane((int32_t)((a >> 32) & 0xffffu)), (int32_t)bytes,
-               0x00020000};
-}
 
-// buffer_load_dwordx4 ... lds (see the gather kernel): lane l copies 16 B at byte
-// offset voff of the resource to LDS address m0 + 16 l; waited with wait_vmcnt.
-__device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t voff, uint32_t m0) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(rsrc), "{m0}"(m0)
-               : "memory");
-}
 
 struct S2 {
   f32x4 t0, t1;
