@@ -98,3 +98,77 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("DSA_MI355X_LIB", str(tmp_path / "nope.so"))
     with pytest.raises(RuntimeError, match="missing"):
         _native.load()
+
+
+def _mla(lib, **kw):
+    a = dict(q=16, kv=16, idx=16, sink=16, out=16, b=1, m=4, h=128, dqk=576, dv=512, kv_dim=576,
+             n_kv=100, topk=64, scale=576 ** -0.5)
+    a.update(kw)
+    return lib.dsa_sparse_mla_fwd(a["q"], a["kv"], a["idx"], a["sink"], a["out"], a["b"], a["m"], a["h"],
+                                  a["dqk"], a["dv"], a["kv_dim"], a["n_kv"], a["topk"], a["scale"], None)
+
+
+def test_sparse_mla_host_checks():
+    """Every rejection happens before any HIP call, so it runs without a GPU."""
+    lib = _native.load()
+    assert _mla(lib, b=-1) == -2
+    assert _mla(lib, n_kv=0) == -2
+    assert _mla(lib, topk=0) == -2
+    assert _mla(lib, dqk=512) == -3          # only d_qk 576 / d_v 512 are built
+    assert _mla(lib, dv=576) == -3
+    assert _mla(lib, kv_dim=512) == -3       # rows narrower than the keys
+    assert _mla(lib, kv_dim=580) == -3       # row stride must be a multiple of 8 channels
+    assert _mla(lib, h=48) == -3             # 64..128 heads in steps of 16
+    assert _mla(lib, h=144) == -3
+    assert _mla(lib, h=72) == -3
+    assert _mla(lib, topk=2049) == -3
+    assert _mla(lib, scale=0.0) == -3
+    assert _mla(lib, scale=float("inf")) == -3
+    assert _mla(lib, n_kv=(1 << 21) + 1) == -3
+    assert _mla(lib, b=0) == 0 and _mla(lib, m=0) == 0
+    assert _mla(lib, q=None) == -1
+    assert _mla(lib, out=None) == -1
+    assert _mla(lib, kv=24) == -6
+
+
+def _ixw(lib, **kw):
+    a = dict(q=16, kv=16, kvbs=8192 * 128, wl=16, scale=0.011, fr=16, mode=1, out=16, b=1, s=8,
+             h=64, d=128, rd=64, T=8192, K=2048, ratio=1, causal=1, offset=0, ws=16, wsb=1 << 20)
+    a.update(kw)
+    return lib.dsa_indexer_score_topk_ws(a["q"], a["kv"], a["kvbs"], a["wl"], a["scale"], a["fr"], a["mode"],
+                                         a["out"], a["b"], a["s"], a["h"], a["d"], a["rd"], a["T"], a["K"],
+                                         a["ratio"], a["causal"], a["offset"], a["ws"], a["wsb"], None)
+
+
+def test_wide_indexer_host_checks():
+    lib = _native.load()
+    assert _ixw(lib, T=8196, kvbs=8196 * 128) == -3  # more than 8192 candidates
+    assert _ixw(lib, T=8190, kvbs=8190 * 128) == -3  # candidate count not a multiple of 4
+    assert _ixw(lib, T=8192, K=4096) == -3           # top-k beyond 2048
+    assert _ixw(lib, K=8193) == -2                   # k > candidates
+    assert _ixw(lib, kvbs=100) == -2
+    assert _ixw(lib, rd=130) == -2
+    assert _ixw(lib, wsb=-1) == -2
+    assert _ixw(lib, ws=24) == -6                    # workspace must be 16-byte aligned
+    assert _ixw(lib, out=None) == -1
+    assert _ixw(lib, s=0) == 0
+
+
+def test_workspace_bytes():
+    lib = _native.load()
+    assert lib.dsa_indexer_workspace_bytes(1, 8192, 64, 128, 8192) == 8192 * 8192 * 2
+    assert lib.dsa_indexer_workspace_bytes(2, 100, 64, 128, 512) == 2 * 100 * 512 * 2
+    assert lib.dsa_indexer_workspace_bytes(8, 2600, 16, 64, 650) == 0   # the 16-head kernel needs none
+    assert lib.dsa_indexer_workspace_bytes(-1, 8, 64, 128, 64) == -1
+
+
+def test_indexer_scores_host_checks():
+    lib = _native.load()
+    args = [16, 16, 650 * 64, 16, 0.03, 16, 1, 16, 1, 8, 16, 64, 32, 650, 4, 1, None]
+    assert lib.dsa_indexer_scores(*args[:7], None, *args[8:]) == -1   # no score buffer
+    bad = list(args)
+    bad[7] = 17                                                          # odd address for bf16 scores
+    assert lib.dsa_indexer_scores(*bad) == -6
+    bad = list(args)
+    bad[13] = 0                                                          # no candidates
+    assert lib.dsa_indexer_scores(*bad) == -2
