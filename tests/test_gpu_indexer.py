@@ -162,6 +162,10 @@ SMALL = [
     (1, 129, 300, 11, 128, 650),
     (4, 1000, 0, 0, 256, 650),
     (1, 2600, 0, 0, 128, 700),
+    # decode at the configs[2] size: one new token per batch at the end of the
+    # 2600-token context (no mask, +offset), and a 40-token chunk before it
+    (8, 1, 2599, 5, 128, 650),
+    (8, 40, 2560, 0, 128, 650),
 ]
 
 

@@ -105,6 +105,7 @@ WIDE = [
     (700, 0, 0, 300, 1),
     (64, 128, 7, 64, 1),
     (256, 0, 0, 96, 2),
+    (4, 8188, 9, 2048, 1),   # decode at the configs[4] size: 4 tokens at the end of 8192
 ]
 
 
