@@ -36,7 +36,7 @@ constexpr int kD = 128;
 #define DSA_SA_NT_STORE 1
 #endif
 #ifndef DSA_SA_TILES_PER_WAVE
-#define DSA_SA_TILES_PER_WAVE 4
+#define DSA_SA_TILES_PER_WAVE 2
 #endif
 
 struct MultParams {
@@ -89,8 +89,11 @@ __device__ __forceinline__ bf16x8 load_row16(const uint16_t* p) {
 // waits only for the first group, stages the kv block in LDS (as a swizzled
 // row copy and as the pre-permuted operand of the second product) and then
 // computes tile by tile while the q loads are still arriving.
+// Four resident workgroups per CU (<= 128 VGPRs, 32 KB LDS each): with two tiles
+// per wave that keeps 128 KB of q loads in flight per CU, which measured faster
+// than three workgroups of four tiles per wave.
 template <int TPW, bool BIGK>
-__global__ __launch_bounds__(256) void sa_mult_kernel(MultParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void sa_mult_kernel(MultParams p) {
   __shared__ u32x4 kraw[32 * 16];  // kv row r chunk c (8 channels) at r*16 + (c ^ (r & 15))
   __shared__ u32x4 img_pv[8][64];  // fragment mt: kv[pi(8g+j)][delta(mt, n)], j = 0..7
   __shared__ u32x4 obuf[4][256];   // per-wave output tile, 16 rows x 16 chunks, chunk ^ row
