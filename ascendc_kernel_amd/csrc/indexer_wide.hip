@@ -43,7 +43,6 @@ constexpr int kMaxT = 8192;
 constexpr int kMaxK = 2048;
 
 typedef short s16v2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 struct WideParams {
   const uint16_t* q;    // [B, S, 64, 128] projected queries (before RoPE)
@@ -64,11 +63,7 @@ struct WideParams {
   int32_t psort;        // power of two >= K (pick buffer length)
 };
 
-
-
-
 __device__ __forceinline__ int swz(int r, int c) { return r * 16 + (c ^ (r & 15)); }
-
 
 // Head of MFMA row R in the wave for head parity y: lane half hf = (R/4)%2 and
 // register r = 4(R/8) + R%4 hold head y + 4hf + 2(r%2) + 8(r/2), so a lane has
@@ -510,7 +505,6 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
                        tmpbuf + tl * p.psort, tt, tok_ok ? p.out + row_bt * p.K : nullptr, p.offset);
   }
 }
-
 
 // Top-K of rows of 16-bit order keys written by ix_wide_kernel: one workgroup
 // (256 threads) per token row. Thread tt holds keys [32 tt, 32 tt + 32) of the row

@@ -36,7 +36,6 @@ constexpr uint32_t kNegHiBits = 0xbf800000u;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 struct GatherParams {
   const uint16_t* q;     // [B, M, H, 128]
@@ -49,7 +48,6 @@ struct GatherParams {
   int32_t xpb;           // XCDs per batch for the block -> token map (0: identity)
   float scale_log2;      // softmax_scale * log2(e)
 };
-
 
 // Output channel of row i of d-tile dt (O^T rows): lane half hf = (i >> 2) & 1
 // gets the contiguous channels 64*hf .. 64*hf + 63 across the four d-tiles.

@@ -52,9 +52,6 @@ struct MlaParams {
   float scale_log2;
 };
 
-
-
-
 struct S2 {
   f32x4 t0, t1;
 };
