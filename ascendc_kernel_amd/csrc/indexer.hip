@@ -152,40 +152,22 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   const int ntile = (nv_max + 31) >> 5;
   const int ntile_all = (p.keys_bytes / 128);
 
-  // Head weights of this half's token, bf16(fp32(wl) * w_scale), as v_dot2
-  // operands for the products of word k of the swapped scores (slots 2k, 2k+1):
-  // wlo[k] = (w(head of slot 2k), 0), whi[k] = (0, w(head of slot 2k+1)).
-  uint32_t wlo[8], whi[8];
-  {
-    uint32_t wb[kH];
-    if (t < p.S) {
-      const u32x4* wp = reinterpret_cast<const u32x4*>(p.wl + ((int64_t)b * p.S + t) * kH);
-      const u32x4 w0 = wp[0], w1 = wp[1];
+  // Head weights of this half's token, bf16(fp32(wl) * w_scale), fp32 copies.
+  float w[kH];
+  if (t < p.S) {
+    const u32x4* wp = reinterpret_cast<const u32x4*>(p.wl + ((int64_t)b * p.S + t) * kH);
+    const u32x4 w0 = wp[0], w1 = wp[1];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        wb[2 * i] = f2bf(bf_lo(w0[i]) * p.wscale);
-        wb[2 * i + 1] = f2bf(bf_hi(w0[i]) * p.wscale);
-        wb[8 + 2 * i] = f2bf(bf_lo(w1[i]) * p.wscale);
-        wb[8 + 2 * i + 1] = f2bf(bf_hi(w1[i]) * p.wscale);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kH; ++i) wb[i] = 0u;
+    for (int i = 0; i < 4; ++i) {
+      w[2 * i] = bf2f(f2bf(bf_lo(w0[i]) * p.wscale));
+      w[2 * i + 1] = bf2f(f2bf(bf_hi(w0[i]) * p.wscale));
+      w[8 + 2 * i] = bf2f(f2bf(bf_lo(w1[i]) * p.wscale));
+      w[8 + 2 * i + 1] = bf2f(f2bf(bf_hi(w1[i]) * p.wscale));
     }
+  } else {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int r = 2 * k;
-      const int h0 = (r < 4) ? r : (r < 8) ? r + 4 : (r < 12) ? r - 4 : r;
-      wlo[k] = wb[h0];
-      whi[k] = wb[h0 + 1] << 16;
-    }
+    for (int i = 0; i < kH; ++i) w[i] = 0.f;
   }
-  // bf16 pairs (1, 0) and (0, 1) kept in SGPRs: as literals the compiler would
-  // encode (1, 0) as the inline constant 1.0, which v_dot2c reads as fp32 bits.
-  uint32_t one_lo_bits = 0x00003f80u, one_hi_bits = 0x3f800000u;
-  asm volatile("" : "+s"(one_lo_bits), "+s"(one_hi_bits));
-  const bf16v2 one_lo = __builtin_bit_cast(bf16v2, one_lo_bits);
-  const bf16v2 one_hi = __builtin_bit_cast(bf16v2, one_hi_bits);
 
   // A operand: row i = lane % 32 is (token t0 + i/16, head i%16); lane holds
   // channels 16ks + 8(lane/32) .. +7 of that row, RoPE applied when asked.
@@ -269,26 +251,21 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
       pk[k] = (uint32_t)sw[0];
       pk[k + 4] = (uint32_t)sw[1];
     }
-    // * w, rounded to bf16 (the products are exact in fp32).
-    bf16v2 pb[8];
+    // * w -> bf16 (the products are exact in fp32), as fp32 values.
+    float v[16];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const bf16v2 pv = __builtin_bit_cast(bf16v2, pk[k]);
-      const float p0 = __builtin_amdgcn_fdot2_f32_bf16(pv, __builtin_bit_cast(bf16v2, wlo[k]), 0.0f, false);
-      const float p1 = __builtin_amdgcn_fdot2_f32_bf16(pv, __builtin_bit_cast(bf16v2, whi[k]), 0.0f, false);
-      pb[k] = __builtin_bit_cast(bf16v2, pack_bf2(p0, p1));
+      const int r = 2 * k;
+      const int h0 = (r < 4) ? r : (r < 8) ? r + 4 : (r < 12) ? r - 4 : r;
+      const uint32_t pb = pack_bf2(bf_lo(pk[k]) * w[h0], bf_hi(pk[k]) * w[h0 + 1]);
+      v[r] = bf_lo(pb);
+      v[r + 1] = bf_hi(pb);
     }
-    // Accumulator j takes heads j, j+4, j+8, j+12 = slots j, j+8, j+4, j+12, all
-    // in half j%2 of words j/2 + {0, 4, 2, 6}; each v_dot2c adds one product.
+    // Head j is in slot j (j<4), j+4 -> slot j+8, j+8 -> slot j+4, j+12 -> slot j+12;
+    // IEEE fp32 adds in torch's order.
     float a4[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bf16v2 sel = (j & 1) ? one_hi : one_lo;
-      float a = __builtin_amdgcn_fdot2_f32_bf16(pb[j >> 1], sel, 0.0f, false);
-      a = __builtin_amdgcn_fdot2_f32_bf16(pb[(j >> 1) + 4], sel, a, false);
-      a = __builtin_amdgcn_fdot2_f32_bf16(pb[(j >> 1) + 2], sel, a, false);
-      a4[j] = __builtin_amdgcn_fdot2_f32_bf16(pb[(j >> 1) + 6], sel, a, false);
-    }
+    for (int j = 0; j < 4; ++j) a4[j] = (((0.0f + v[j]) + v[j + 8]) + v[j + 4]) + v[j + 12];
     const float tot = ((a4[0] + a4[1]) + a4[2]) + a4[3];
     uint16_t sc = f2bf(tot);
     const int c = 32 * tile + hl;

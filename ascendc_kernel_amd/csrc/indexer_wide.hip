@@ -21,8 +21,8 @@
 //   S[32 heads x 32 candidates] = Q[32 x 128] . K^T   (8 x mfma 32x32x16)
 // with its 32 head rows permuted so that every lane holds, for one candidate,
 // 2 of its thread's 4 accumulators complete (8 heads each, in order): the
-// relu/w/bf16 chain and the sums are lane-local (v_dot2 on packed bf16 pairs
-// does the exact products and the fp32 additions), one v_permlane32_swap joins
+// relu/w/bf16 chain and the sums are lane-local (relu with v_pk_max_i16 on the
+// packed bf16 scores, exact fp32 products, IEEE fp32 adds), one v_permlane32_swap joins
 // the lane halves, and the even/odd totals meet in LDS. Scores become 16-bit
 // order keys in LDS; per token a two-pass 8-bit radix select finds the k-th key,
 // the picks are compacted ([> k-th] then [== k-th] in index order) and put in
@@ -391,8 +391,8 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
       qa[ks] = __builtin_bit_cast(bf16x8, v);
     }
   }
-  // Head weights of the lane's 16 heads as dot2 operands: wlo[m] = (w(h0), 0),
-  // whi[m] = (0, w(h0 + 2)) with h0 = y + 4hf + 8m.
+  // Head weights of the lane's 16 heads (bf16 bits): wlo[m] = w(h0) in the low half,
+  // whi[m] = w(h0 + 2) in the high half, h0 = y + 4hf + 8m.
   uint32_t wlo[8], whi[8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
@@ -405,12 +405,6 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     wlo[m] = w0;
     whi[m] = w1 << 16;
   }
-  // bf16 pairs (1, 0) and (0, 1) in SGPRs: as literals the compiler would encode
-  // (1, 0) as the inline constant 1.0, which v_dot2c reads as the fp32 pattern.
-  uint32_t one_lo_bits = 0x00003f80u, one_hi_bits = 0x3f800000u;
-  asm volatile("" : "+s"(one_lo_bits), "+s"(one_hi_bits));
-  const bf16v2 one_lo = __builtin_bit_cast(bf16v2, one_lo_bits);
-  const bf16v2 one_hi = __builtin_bit_cast(bf16v2, one_hi_bits);
 
   // Tile copies: wave wi moves unit wi (rows 4wi .. 4wi+3 of the tile).
   const i32x4 rsrc = make_rsrc(p.kv + (int64_t)b * p.kvbs, (uint32_t)p.T * (uint32_t)(kWD * 2));
@@ -474,12 +468,12 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     for (int m = 0; m < 8; ++m) {
       s16v2 pk = __builtin_bit_cast(s16v2, pack_bf2(s[2 * m], s[2 * m + 1]));
       pk = __builtin_elementwise_max(pk, (s16v2){0, 0});  // relu on the bf16 bit patterns
-      const bf16v2 pv = __builtin_bit_cast(bf16v2, pk);
-      const float p0 = __builtin_amdgcn_fdot2_f32_bf16(pv, __builtin_bit_cast(bf16v2, wlo[m]), 0.0f, false);
-      const float p1 = __builtin_amdgcn_fdot2_f32_bf16(pv, __builtin_bit_cast(bf16v2, whi[m]), 0.0f, false);
-      const bf16v2 pp = __builtin_bit_cast(bf16v2, pack_bf2(p0, p1));
-      acc_a = __builtin_amdgcn_fdot2_f32_bf16(pp, one_lo, acc_a, false);
-      acc_b = __builtin_amdgcn_fdot2_f32_bf16(pp, one_hi, acc_b, false);
+      // bf16 x bf16 products are exact in fp32; each is rounded to bf16 and added
+      // with an IEEE fp32 add (v_dot2c's accumulation does not always round like one).
+      const uint32_t pv = __builtin_bit_cast(uint32_t, pk);
+      const uint32_t pp = pack_bf2(bf_lo(pv) * bf_lo(wlo[m]), bf_hi(pv) * bf_hi(whi[m]));
+      acc_a = acc_a + bf_lo(pp);
+      acc_b = acc_b + bf_hi(pp);
     }
     // Lower lanes hold accumulators 0, 1; upper lanes 2, 3 of the same candidate.
     const float a01 = acc_a + acc_b;

@@ -122,9 +122,12 @@ def test_wide_shapes_and_modes(gpu, case):
     _check_equal(m(x, qr, start_pos, offset), r(x, qr, start_pos, offset), f"wide{case}")
 
 
-def test_full_shape_c5_indexer(gpu):
+@pytest.mark.parametrize("input_seed", [43, None])
+def test_full_shape_c5_indexer(gpu, input_seed):
     """configs[4] indexer: x[1,8192,7168], qr[1,8192,1536], kv_cache[1,8192,128], W ~ N(0, 0.02),
-    causal, top-2048, ratio 1, rope_head_dim 64."""
+    causal, top-2048, ratio 1, rope_head_dim 64. input_seed None draws x and qr right after
+    the model (the draw in which an accumulation through v_dot2c_f32_bf16 once changed the
+    top-k of one row; the kernels now add with IEEE fp32 adds)."""
     torch.manual_seed(42)
     init = t2.get_c5_init_inputs(device=gpu)
     m = t2.Model(*init).to(gpu)
@@ -132,12 +135,13 @@ def test_full_shape_c5_indexer(gpu):
     with torch.no_grad():
         for p in (m.wq_b.weight, m.weights_proj.weight):
             p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(torch.bfloat16))
+    if input_seed is not None:
+        torch.manual_seed(input_seed)
+    x, qr, sp, off = t2.get_c5_inputs(device=gpu)
     r = oix.IndexerRef(*init).to(gpu)
     r.wq_b.weight.data.copy_(m.wq_b.weight.data)
     r.weights_proj.weight.data.copy_(m.weights_proj.weight.data)
-    torch.manual_seed(43)
-    x, qr, sp, off = t2.get_c5_inputs(device=gpu)
-    _say("case c5 indexer full shape")
+    _say("case c5 indexer full shape", input_seed)
     with torch.no_grad():
         got = m(x, qr, sp, off)
         torch.cuda.synchronize()
