@@ -131,10 +131,14 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   constexpr int KP = 32 * E;  // sort size per half-wave
   const int lane = threadIdx.x & 63;
   const int wi = threadIdx.x >> 6;
-  const int64_t gw = (int64_t)blockIdx.x * 4 + wi;
-  if (gw >= (int64_t)p.B * p.npairs) return;
-  const int pr = p.npairs - 1 - (int)(gw / p.B);  // longest rows first
-  const int b = (int)(gw % p.B);
+  // A workgroup = 4 consecutive token pairs (8 tokens) of one batch, so that its
+  // waves share the candidate tiles; groups from the end of the sequence (the
+  // longest causal rows) start first. Waves past the last pair still take part in
+  // the tile copies and barriers (their tokens are >= S and produce nothing).
+  const int ngroups = (p.npairs + 3) >> 2;
+  const int b = (int)(blockIdx.x % (unsigned)p.B);
+  const int grp = ngroups - 1 - (int)(blockIdx.x / (unsigned)p.B);
+  const int pr = 4 * grp + wi;
   const int t0 = 2 * pr;
   const int half = lane >> 5, hl = lane & 31;
   const int t = t0 + half;
@@ -147,10 +151,13 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   uint32_t* mysbuf = sbuf + KP * half;
 
   const int nv = n_valid(p, t);
-  const int tlast = (t0 + 1 < p.S) ? t0 + 1 : t0;
-  const int nv_max = n_valid(p, tlast) > n_valid(p, t0) ? n_valid(p, tlast) : n_valid(p, t0);
-  const int ntile = (nv_max + 31) >> 5;
+  // Tiles of the workgroup: up to the valid candidates of its last token (the
+  // count grows with t).
+  const int tg_last = min(2 * (4 * grp + 3) + 1, p.S - 1);
+  const int ntile = (n_valid(p, tg_last) + 31) >> 5;
   const int ntile_all = (p.keys_bytes / 128);
+  // Candidate tiles (32 rows x 128 B) in a 4-slot LDS ring after the wave areas.
+  uint8_t* ring = smem + 4 * (size_t)p.wave_bytes;
 
   // Head weights of this half's token, bf16(fp32(wl) * w_scale), fp32 copies.
   float w[kH];
@@ -211,27 +218,41 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   *reinterpret_cast<u32x4*>(myhist + 8 * hl + 4) = u32x4{0u, 0u, 0u, 0u};
   lds_fence();
 
-  // Candidate rows through a buffer resource: rows >= T read as zero. The next
-  // tile's operands are requested before the current tile is processed.
-  const __amdgpu_buffer_rsrc_t krs = buf_rsrc(p.kv + (int64_t)b * p.kvbs, (uint32_t)p.T * kD * 2);
+  // Tile n is copied by buffer_load ... lds into ring slot n % 4: wave wi moves rows
+  // 8wi .. 8wi+7 (lane l: row 8wi + l/8, 16-byte chunk (l%8) ^ (row%8), so chunk c of
+  // row r sits at position 8r + (c ^ (r%8)) and the fragment reads below spread over
+  // all banks). Rows >= T read as zero through the resource's range.
+  const i32x4 krs = make_rsrc(p.kv + (int64_t)b * p.kvbs, (uint32_t)p.T * (uint32_t)(kD * 2));
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;
+  const int wis = __builtin_amdgcn_readfirstlane(wi);
+  const int crow = 8 * wis + (lane >> 3);
+  const uint32_t coff = (uint32_t)(crow * kD + 8 * ((lane & 7) ^ (crow & 7))) * 2u;
+  auto issue = [&](int n) {
+    lds_dma16(krs, (uint32_t)(32 * n * kD * 2) + coff, ring_lds + 4096u * (uint32_t)(n & 3) + 1024u * (uint32_t)wis);
+  };
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+    if (j < ntile) issue(j);
+  // Consume the compiler-tracked loads here: its own vmcnt(0) for them (which also
+  // covers the copies just issued) then stays out of the loop.
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qa[ks]));
+#pragma unroll
+  for (int i = 0; i < kH; ++i) asm volatile("" ::"v"(w[i]));
+  // B operand: candidate 32*tile + lane%32, channels 16ks + 8(lane/32) .. +7.
   const int kcol = lane & 31;
   const int khalf = lane >> 5;
-  auto load_kb = [&](int tile, bf16x8* kb) {
-    // B operand: candidate 32*tile + lane%32, channels 16ks + 8(lane/32) .. +7.
-    const int off = ((32 * tile + kcol) * kD + 8 * khalf) * 2;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      kb[ks] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 32 * ks, 0, 0));
-  };
-  bf16x8 kb[4], kn[4];
-  load_kb(0, kb);
   for (int tile = 0; tile < ntile; ++tile) {
-    load_kb(tile + 1, kn);
+    if (tile + 2 < ntile) wait_vmcnt<2>();
+    else if (tile + 1 < ntile) wait_vmcnt<1>();
+    else wait_vmcnt<0>();
+    __syncthreads();  // tile `tile` is in LDS for every wave; the slot of tile-1 is free
+    if (tile + 3 < ntile) issue(tile + 3);
+    const u32x4* kt = reinterpret_cast<const u32x4*>(ring + 4096 * (tile & 3));
     f32x16 acc = {};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma32x32x16(qa[ks], kb[ks], acc);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kb[ks] = kn[ks];
+    for (int ks = 0; ks < 4; ++ks)
+      acc = mfma32x32x16(qa[ks], __builtin_bit_cast(bf16x8, kt[8 * kcol + ((2 * ks + khalf) ^ (kcol & 7))]), acc);
 
     // The einsum's bf16 rounding, then relu on the bf16 bit patterns (both heads
     // of a word at once): word k holds slots 2k, 2k+1.
@@ -531,10 +552,10 @@ int launch_ix(const void* q, const void* kv_cache, int64_t kv_batch_stride, cons
   int E = 1;
   while (32 * E < k_out) E <<= 1;
   p.wave_bytes = p.keys_bytes + 2048 + 8 * 32 * E;
-  const size_t smem = (size_t)p.wave_bytes * 4;
+  const size_t smem = (size_t)p.wave_bytes * 4 + 4 * 4096;  // 4 wave areas + the tile ring
   if (smem > 64 * 1024) return DSA_ERR_UNSUPPORTED;
-  const int64_t waves = (int64_t)b * p.npairs;
-  const int64_t blocks = (waves + 3) / 4;
+  const int64_t blocks = (int64_t)b * ((p.npairs + 3) / 4);  // 4 token pairs of one batch each
+  if (blocks > INT32_MAX) return DSA_ERR_SHAPE;
   hipStream_t st = (hipStream_t)stream;
   switch (E) {
     case 1: hipLaunchKernelGGL(ix_score_topk_kernel<1>, dim3((unsigned)blocks), dim3(256), smem, st, p); break;
