@@ -443,30 +443,40 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     }
   };
 
-  // Tiles in groups of kRingW, so that the ring slot (and with it every LDS
-  // operand address) is a compile-time offset from loop-invariant lane addresses.
+  // Software pipeline: iteration n issues the products of tile n + 1 one k-step at a
+  // time, each followed by one step of tile n's rounding chain (plain VALU work, which
+  // the SIMD can issue while the matrix core runs). One 16-byte operand read at a
+  // time keeps the register count low enough for two workgroups per CU. Iteration n
+  // waits for tile n + 1 and refills the slot of tile n - 1, whose products ran two
+  // iterations ago. Tiles go in groups of kRingW so every ring slot is a constant.
+  f32x16 s_cur = {};
+  if (ntiles > 0) {
+    if (ntiles > 2) wait_vmcnt<2>();
+    else if (ntiles > 1) wait_vmcnt<1>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      s_cur = mfma32x32x16(qa[ks], __builtin_bit_cast(bf16x8, ring[swz(col, 2 * ks + hf)]), s_cur);
+  }
   for (int n0 = 0; n0 < ntiles; n0 += kRingW) {
 #pragma unroll
    for (int j = 0; j < kRingW; ++j) {
     const int n = n0 + j;
     if (n >= ntiles) break;
-    if (n + 2 < ntiles) wait_vmcnt<2>();
-    else if (n + 1 < ntiles) wait_vmcnt<1>();
+    if (n + 2 < ntiles) wait_vmcnt<1>();
     else wait_vmcnt<0>();
-    __syncthreads();  // tile n is in LDS; tile n-1's buffer and odd totals are consumed/visible
+    __syncthreads();  // tile n+1 is in LDS; tile n-1's slot and odd totals are consumed/visible
     if (n > 0) finalize(n - 1);
     if (n + kRingW - 1 < ntiles) issue(n + kRingW - 1);
-    const u32x4* kt = ring + j * 512;
-    f32x16 s = {};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 bk = __builtin_bit_cast(bf16x8, kt[swz(col, 2 * ks + hf)]);
-      s = mfma32x32x16(qa[ks], bk, s);
-    }
+    // (after the last tile this reads a stale slot; the result is not used)
+    const u32x4* kt = ring + ((j + 1) % kRingW) * 512;
+    f32x16 s_nx = {};
     float acc_a = 0.f, acc_b = 0.f;
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      s16v2 pk = __builtin_bit_cast(s16v2, pack_bf2(s[2 * m], s[2 * m + 1]));
+      s_nx = mfma32x32x16(qa[m], __builtin_bit_cast(bf16x8, kt[swz(col, 2 * m + hf)]), s_nx);
+      s16v2 pk = __builtin_bit_cast(s16v2, pack_bf2(s_cur[2 * m], s_cur[2 * m + 1]));
       pk = __builtin_elementwise_max(pk, (s16v2){0, 0});  // relu on the bf16 bit patterns
       // bf16 x bf16 products are exact in fp32; each is rounded to bf16 and added
       // with an IEEE fp32 add (v_dot2c's accumulation does not always round like one).
@@ -475,6 +485,7 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
       acc_a = acc_a + bf_lo(pp);
       acc_b = acc_b + bf_hi(pp);
     }
+    s_cur = s_nx;
     // Lower lanes hold accumulators 0, 1; upper lanes 2, 3 of the same candidate.
     const float a01 = acc_a + acc_b;
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a01), __float_as_uint(a01), false, false);
