@@ -63,7 +63,7 @@ template <int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW >= 2 ? 2 : 1)))
 void sa_gather_kernel(GatherParams p) {
   __shared__ u32x4 ring[kRing][kKB * 16];  // kRing blocks of 32 gathered rows (8 KB each)
-  __shared__ int32_t nblk_sh;
+  __shared__ int32_t nblk_w[NW];  // per wave: blocks up to its last valid slot
   extern __shared__ int32_t slot[];         // the token's slot indices (masked -> -1)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -85,35 +85,56 @@ void sa_gather_kernel(GatherParams p) {
   const bool hvalid = hbase + col < p.H;  // the last wave may cover fewer than 32 heads
   const uint16_t* kvb = p.kv + (int64_t)b * p.NKV * kD;
 
-  if (tid == 0) nblk_sh = 0;
-  __syncthreads();
-  // Slot indices -> LDS; out-of-range indices count as masked. Blocks after the
-  // last one holding a valid slot are neither loaded nor computed.
-  const int nblk = (p.TOPK + kKB - 1) / kKB;
-  int last = 0;
-  for (int s = tid; s < nblk * kKB; s += 64 * NW) {
-    int v = -1;
-    if (s < p.TOPK) {
-      v = p.idx[tok * p.TOPK + s];
-      if (v >= p.NKV) v = -1;
-    }
-    slot[s] = v;
-    if (v >= 0) last = s / kKB + 1;
-  }
-  if (last > 0) atomicMax(&nblk_sh, last);
-
+  // The token's global reads (Q^T, the sink, the slot indices) are all issued
+  // before any of them is waited for: one memory latency instead of one per
+  // round of the slot loop.
   // Q^T fragments (B operand of the first product): head hbase+col, channels
   // 16ks + 8hf .. +7.
+  // Lanes of heads >= H (the last wave when H % 32 != 0) load head 0's row: their
+  // MFMA columns and softmax stay separate from the valid heads' and are never
+  // stored; loading unconditionally keeps the loads out of branches (whose joins
+  // would make the compiler wait for them at once).
   bf16x8 qf[8];
   {
     const uint16_t* qrow = p.q + (tok * p.H + (hvalid ? hbase + col : 0)) * kD + 8 * hf;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
-      qf[ks] = hvalid ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + 16 * ks))
-                      : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+      qf[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + 16 * ks));
   }
+  const float sink_raw = p.sink[hvalid ? hbase + col : 0];  // unconditional: no wait in a branch
+  // Slot indices -> LDS, 8 per thread in flight at a time; out-of-range indices
+  // count as masked. Blocks after the last one holding a valid slot are neither
+  // loaded nor computed.
+  const int nblk = (p.TOPK + kKB - 1) / kKB;
+  int last = 0;
+  auto slot_chunk = [&](const int s0) {
+    int v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + 64 * NW * u + tid;
+      v[u] = p.idx[tok * p.TOPK + min(s, p.TOPK - 1)];  // unconditional (see q)
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + 64 * NW * u + tid;
+      if (s < nblk * kKB) {
+        const int w = (s < p.TOPK && v[u] < p.NKV) ? v[u] : -1;
+        slot[s] = w;
+        if (w >= 0) last = s / kKB + 1;
+      }
+    }
+  };
+  // the first chunk outside the loop, so that nothing waits for Q^T before its loads issue
+  slot_chunk(0);
+  for (int s0 = 8 * 64 * NW; s0 < nblk * kKB; s0 += 8 * 64 * NW) slot_chunk(s0);
+  // Blocks to compute: the maximum of `last` over the wave, then over the waves.
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) last = max(last, __shfl_xor(last, m, 64));
+  if (lane == 0) nblk_w[wi] = last;
   __syncthreads();
-  const int nb = nblk_sh;
+  int nb = nblk_w[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) nb = max(nb, nblk_w[w]);
 
   // A block is 8 units of 4 rows (1 KB); one global_load_lds_dwordx4 moves a
   // unit: lane l writes LDS chunk 64u + l, i.e. row 4u + l/16, swizzled chunk
@@ -148,7 +169,7 @@ void sa_gather_kernel(GatherParams p) {
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
-  const float sink_l2 = hvalid ? p.sink[hbase + col] * kLog2e : 0.f;
+  const float sink_l2 = hvalid ? sink_raw * kLog2e : 0.f;
   const float c2 = p.scale_log2;  // > 0 (checked by the host)
   float m_run = sink_l2;   // running max (log2 units) incl. the sink
   float l_run = 0.f;       // this lane's partial sum of exp2(s - m_run)
@@ -248,6 +269,10 @@ void sa_gather_kernel(GatherParams p) {
 
     // S of the next block (after the last block this reads a stale buffer and
     // the result is unused), independent of the softmax below.
+    // The wave runs at raised priority from here to the PV products: on a SIMD
+    // shared with another workgroup's wave, the softmax (VALU) of one wave then
+    // tends to issue while the other's products occupy the matrix cores (~4 %).
+    __builtin_amdgcn_s_setprio(1);
     const f32x16 s_next = qk(ring[(j + 1) % kRing]);
 
     float pe[16];
@@ -278,6 +303,7 @@ void sa_gather_kernel(GatherParams p) {
     // transposed reads give keys 16st + 4hf + (0..3) and 16st + 8 + 4hf + (0..3).
     // Supplier lane u of a 16-lane group reads 4 channels of one key row:
     // key = base + (u >> 2), channels out_ch(dt, 16*g16 + 4*(u & 3)) .. +3.
+    __builtin_amdgcn_s_setprio(0);
     const int u = lane & 15, g16 = (lane >> 4) & 1;
     const uint16_t* kvh = reinterpret_cast<const uint16_t*>(ring[j]);
 #pragma unroll

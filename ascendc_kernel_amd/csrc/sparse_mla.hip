@@ -63,7 +63,7 @@ void sa_mla_kernel(MlaParams p) {
   uint8_t* ring = smem;                                                   // [kRingM][kBlkBytes]
   int32_t* slot = reinterpret_cast<int32_t*>(smem + kRingM * kBlkBytes);  // [nblk * 32]
   const int nblk = (p.TOPK + kKB - 1) / kKB;
-  int32_t* nblk_sh = slot + nblk * kKB;
+  int32_t* nblk_sh = slot + nblk * kKB;  // [NW] blocks up to each wave's last valid slot
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -73,33 +73,46 @@ void sa_mla_kernel(MlaParams p) {
   const int n = lane & 15;  // head 16wi + n
   const int g = lane >> 4;  // lane group: k-slice 8g..8g+7, C rows 4g..4g+3
   const int head = 16 * wi + n;
-  const bool hvalid = head < p.H;
 
-  if (tid == 0) *nblk_sh = 0;
-  __syncthreads();
-  int last = 0;
-  for (int s = tid; s < nblk * kKB; s += 64 * NW) {
-    int v = -1;
-    if (s < p.TOPK) {
-      v = p.idx[tok * p.TOPK + s];
-      if (v >= p.NKV) v = -1;
-    }
-    slot[s] = v;
-    if (v >= 0) last = s / kKB + 1;
-  }
-  if (last > 0) atomicMax(nblk_sh, last);
-
-  // Q^T fragments (B operand): head `head`, channels 32ks + 8g .. +7.
+  // The token's global reads (Q^T, the sink, the slot indices) are all issued
+  // before any of them is waited for. Q^T fragments (B operand): head `head`,
+  // channels 32ks + 8g .. +7; every head is valid (H % 16 == 0).
   bf16x8 qf[kKS];
   {
-    const uint16_t* qrow = p.q + (tok * p.H + (hvalid ? head : 0)) * kDQK + 8 * g;
+    const uint16_t* qrow = p.q + (tok * p.H + head) * kDQK + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < kKS; ++ks)
-      qf[ks] = hvalid ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + 32 * ks))
-                      : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+      qf[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + 32 * ks));
   }
+  const float sink_raw = p.sink[head];
+  // Slot indices -> LDS, 8 per thread in flight at a time (loads unconditional,
+  // clamped to the row, so that none sits in a branch).
+  int last = 0;
+  auto slot_chunk = [&](const int s0) {
+    int v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + 64 * NW * u + tid;
+      v[u] = p.idx[tok * p.TOPK + min(s, p.TOPK - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + 64 * NW * u + tid;
+      if (s < nblk * kKB) {
+        const int w = (s < p.TOPK && v[u] < p.NKV) ? v[u] : -1;
+        slot[s] = w;
+        if (w >= 0) last = s / kKB + 1;
+      }
+    }
+  };
+  slot_chunk(0);
+  for (int s0 = 8 * 64 * NW; s0 < nblk * kKB; s0 += 8 * 64 * NW) slot_chunk(s0);
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) last = max(last, __shfl_xor(last, m, 64));
+  if (lane == 0) nblk_sh[wi] = last;
   __syncthreads();
-  const int nb = *nblk_sh;
+  int nb = nblk_sh[0];
+  for (int w = 1; w < NW; ++w) nb = max(nb, nblk_sh[w]);
 
   // Copies: unit u covers chunk positions 64u .. 64u+63 of a block buffer
   // (position P = row * 73 + chunk). Wave wi moves units wi, wi + NW, ...; every
@@ -135,7 +148,7 @@ void sa_mla_kernel(MlaParams p) {
   f32x4 o[kCT];
 #pragma unroll
   for (int ct = 0; ct < kCT; ++ct) o[ct] = f32x4{};
-  const float sink_l2 = hvalid ? p.sink[head] * kLog2e : 0.f;
+  const float sink_l2 = sink_raw * kLog2e;
   const float c2 = p.scale_log2;  // > 0 (checked by the host)
   float m_run = sink_l2;
   float l_run = 0.f;
@@ -321,7 +334,7 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
   p.kv_dim = (int32_t)kv_dim;
   p.scale_log2 = softmax_scale * kLog2e;
   const int64_t nblk = (topk + kKB - 1) / kKB;
-  const size_t smem = (size_t)kRingM * kBlkBytes + (size_t)nblk * kKB * 4 + 16;
+  const size_t smem = (size_t)kRingM * kBlkBytes + (size_t)nblk * kKB * 4 + 32;  // + per-wave counts
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)(b * m));
   switch (h / 16) {

@@ -163,6 +163,11 @@ GATHER_CASES = [
     (2, 16, 48, 128, 64, 24, 0.3, -1.0),
     (1, 5, 128, 1000, 2048, 25, 0.5, 0.5),
     (1, 3, 64, 40, 1, 26, 0.0, 0.0),
+    # odd token count, topk 1024 and 2048 with 64 heads, 3 batches (no XCD map)
+    (2, 37, 64, 300, 100, 28, 0.1, 0.5),
+    (1, 13, 64, 2000, 1024, 29, 0.3, 0.0),
+    (3, 6, 48, 200, 70, 30, 0.0, 1.0),
+    (2, 64, 64, 5000, 2048, 31, 0.2, 0.0),
 ]
 
 
