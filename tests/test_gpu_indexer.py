@@ -122,19 +122,22 @@ def _check_equal(got, want, name):
     assert eq, name
 
 
-def test_full_shape_c3(gpu):
-    """configs[2]: x[8,2600,1024], qr[8,2600,256], kv_cache[8,650,64], W ~ N(0, 0.02)."""
+@pytest.mark.parametrize("seeds", [(42, 5, 43), (1, 11, 12), (2, 21, 22)])
+def test_full_shape_c3(gpu, seeds):
+    """configs[2]: x[8,2600,1024], qr[8,2600,256], kv_cache[8,650,64], W ~ N(0, 0.02);
+    seeds = (kv_cache / constructor, weights, inputs)."""
+    ctor_seed, w_seed, in_seed = seeds
     args = t2._make_args()
-    m, r = _pair(args, 42, 8, 650, gpu)
-    g = torch.Generator().manual_seed(5)
+    m, r = _pair(args, ctor_seed, 8, 650, gpu)
+    g = torch.Generator().manual_seed(w_seed)
     with torch.no_grad():
         for p in (m.wq_b.weight, m.weights_proj.weight):
             p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(torch.bfloat16))
     r.wq_b.weight.data.copy_(m.wq_b.weight.data)
     r.weights_proj.weight.data.copy_(m.weights_proj.weight.data)
-    torch.manual_seed(43)
+    torch.manual_seed(in_seed)
     x, qr, sp, off = t2.get_inputs(device=gpu)
-    _say("case c3 full shape")
+    _say("case c3 full shape", seeds)
     got = m(x, qr, sp, off)
     want = r(x, qr, sp, off)
     torch.cuda.synchronize()

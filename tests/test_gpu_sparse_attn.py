@@ -43,10 +43,11 @@ def _case(b, m, h, n_kv, topk, seed, masked=0.0, sink_scale=0.0, d=128, dev="cud
     return q.to(dev), kv.to(dev), idx.to(dev), sink.to(dev)
 
 
-def test_full_shape_c2(gpu):
+@pytest.mark.parametrize("seed", [42, 7])
+def test_full_shape_c2(gpu, seed):
     """configs[1]: q[8,2600,64,128], kv[8,32,128], idx[8,2600,16] with replacement."""
-    _say("case c2 full shape seed 42")
-    torch.manual_seed(42)
+    _say("case c2 full shape seed", seed)
+    torch.manual_seed(seed)
     q, kv, idx = [x.to(gpu) for x in t1.get_inputs()]
     m = t1.Model(*t1.get_init_inputs()).to(gpu)
     out = m(q, kv, idx)
@@ -192,12 +193,14 @@ def test_gather_equals_multiplicity(gpu):
     _compare(b_, ref, "mult-small")
 
 
-def test_full_shape_c4_gather(gpu):
-    """q[4,4096,64,128], kv[4,8192,128], topk 512 drawn from [0, t], -1 padded."""
-    g = torch.Generator().manual_seed(42)
-    _say("case c4 inputs")
+@pytest.mark.parametrize("seed,sink_scale", [(42, 0.0), (3, 1.0)])
+def test_full_shape_c4_gather(gpu, seed, sink_scale):
+    """q[4,4096,64,128], kv[4,8192,128], topk 512 drawn from [0, t], -1 padded
+    (and once with a non-zero sink)."""
+    g = torch.Generator().manual_seed(seed)
+    _say("case c4 inputs", seed, sink_scale)
     q, kv, idx = osa.gather_inputs(4, 4096, 64, 128, 8192, 512, generator=g, device=gpu)
-    sink = torch.zeros(64, device=gpu)
+    sink = (torch.randn(64, generator=g) * sink_scale).to(gpu)
     _say("case c4 kernel")
     out = _native.sparse_attn_fwd(q, kv, idx, sink, 128 ** -0.5)
     torch.cuda.synchronize()
