@@ -449,7 +449,9 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
   // time keeps the register count low enough for two workgroups per CU. Iteration n
   // waits for tile n + 1 and refills the slot of tile n - 1, whose products ran two
   // iterations ago. Tiles go in groups of kRingW so every ring slot is a constant.
-  f32x16 s_cur = {};
+  // The scores of consecutive tiles alternate between two accumulator sets (sA, sB),
+  // so no register copy is needed between iterations.
+  f32x16 sA = {}, sB = {};
   if (ntiles > 0) {
     if (ntiles > 2) wait_vmcnt<2>();
     else if (ntiles > 1) wait_vmcnt<1>();
@@ -457,13 +459,10 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
-      s_cur = mfma32x32x16(qa[ks], __builtin_bit_cast(bf16x8, ring[swz(col, 2 * ks + hf)]), s_cur);
+      sA = mfma32x32x16(qa[ks], __builtin_bit_cast(bf16x8, ring[swz(col, 2 * ks + hf)]), sA);
   }
-  for (int n0 = 0; n0 < ntiles; n0 += kRingW) {
-#pragma unroll
-   for (int j = 0; j < kRingW; ++j) {
-    const int n = n0 + j;
-    if (n >= ntiles) break;
+  // Iteration n: s_cur holds S of tile n, s_nx receives S of tile n + 1.
+  auto step = [&](const int n, const int j, const f32x16& s_cur, f32x16& s_nx) {
     if (n + 2 < ntiles) wait_vmcnt<1>();
     else wait_vmcnt<0>();
     __syncthreads();  // tile n+1 is in LDS; tile n-1's slot and odd totals are consumed/visible
@@ -471,7 +470,7 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     if (n + kRingW - 1 < ntiles) issue(n + kRingW - 1);
     // (after the last tile this reads a stale slot; the result is not used)
     const u32x4* kt = ring + ((j + 1) % kRingW) * 512;
-    f32x16 s_nx = {};
+    s_nx = f32x16{};
     float acc_a = 0.f, acc_b = 0.f;
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
@@ -485,7 +484,6 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
       acc_a = acc_a + bf_lo(pp);
       acc_b = acc_b + bf_hi(pp);
     }
-    s_cur = s_nx;
     // Lower lanes hold accumulators 0, 1; upper lanes 2, 3 of the same candidate.
     const float a01 = acc_a + acc_b;
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a01), __float_as_uint(a01), false, false);
@@ -495,7 +493,16 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     } else {
       t0val = ty;
     }
-   }
+  };
+  static_assert(kRingW % 2 == 0, "the accumulator sets alternate within a ring group");
+  for (int n0 = 0; n0 < ntiles; n0 += kRingW) {
+#pragma unroll
+    for (int j = 0; j < kRingW; ++j) {
+      const int n = n0 + j;
+      if (n >= ntiles) break;
+      if ((j & 1) == 0) step(n, j, sA, sB);
+      else step(n, j, sB, sA);
+    }
   }
   __syncthreads();
   if (ntiles > 0) finalize(ntiles - 1);
