@@ -30,6 +30,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-file additions. indexer.hip: keep MFMA accumulators in VGPRs (the compiler
+# otherwise places the score kernel's accumulator in AGPRs and copies it out with
+# 16 v_accvgpr_read per tile; measured ~2 % faster, identical results).
+EXTRA_FLAGS = {
+    "indexer.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and os.path.exists(cand):
@@ -42,7 +50,7 @@ def sources() -> list[str]:
 
 
 def _compile(src: str, obj: str) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
