@@ -155,27 +155,41 @@ void sa_mla_kernel(MlaParams p) {
 
   // S^T of the block in buffer kvl: tile kt has keys 16kt + (lane%16) as A rows,
   // channels 32ks + 8g; the lane's results are keys 16kt + 4g + r of head n.
+  // Key tile 0 then key tile 1, one K fragment read ahead of its product (order
+  // pinned below), so the LDS latency overlaps the matrix work.
   auto qk = [&](const uint8_t* kvl) {
     S2 acc = {f32x4{}, f32x4{}};
     const u32x4* r0 = reinterpret_cast<const u32x4*>(kvl) + n * kRowC + g;
-    const u32x4* r1 = r0 + 16 * kRowC;
+    auto frag = [&](int i) {  // i = 18 kt + ks
+      return __builtin_bit_cast(bf16x8, r0[(i >= kKS ? 16 * kRowC : 0) + 4 * (i % kKS)]);
+    };
+    bf16x8 a_cur = frag(0);
 #pragma unroll
-    for (int ks = 0; ks < kKS; ++ks) {
-      acc.t0 = mfma16x16x32(__builtin_bit_cast(bf16x8, r0[4 * ks]), qf[ks], acc.t0);
-      acc.t1 = mfma16x16x32(__builtin_bit_cast(bf16x8, r1[4 * ks]), qf[ks], acc.t1);
+    for (int i = 0; i < 2 * kKS; ++i) {
+      bf16x8 a_nxt = a_cur;
+      if (i + 1 < 2 * kKS) a_nxt = frag(i + 1);
+      if (i < kKS) acc.t0 = mfma16x16x32(a_cur, qf[i], acc.t0);
+      else acc.t1 = mfma16x16x32(a_cur, qf[i - kKS], acc.t1);
+      a_cur = a_nxt;
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * kKS - 1; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     return acc;
   };
 
-  int rv[kUnitsW];
 #pragma unroll
   for (int j = 0; j < kRingM - 1; ++j) {
     if (j < nb) {
+      int rv[kUnitsW];
       rows_of(j, rv);
       issue(j, rv);
     }
   }
-  if (nb > 0) rows_of(min(kRingM - 1, nb - 1), rv);
   int vslot = slot[lane & 31];
 #pragma unroll
   for (int ks = 0; ks < kKS; ++ks) asm volatile("" ::"v"(qf[ks]));
@@ -195,9 +209,12 @@ void sa_mla_kernel(MlaParams p) {
       if (kb + 2 < nb) wait_vmcnt<kUnitsW>();
       else wait_vmcnt<0>();
       __syncthreads();  // block kb+1 is in LDS; block kb-1's buffer is free
-      if (kb + kRingM - 1 < nb) issue(kb + kRingM - 1, rv);
+      if (kb + kRingM - 1 < nb) {
+        int rv[kUnitsW];
+        rows_of(kb + kRingM - 1, rv);
+        issue(kb + kRingM - 1, rv);
+      }
       vm_next = (uint32_t)__ballot(vslot >= 0);
-      rows_of(min(kb + kRingM, nb - 1), rv);
       vslot = slot[min(kb + 2, nb - 1) * kKB + (lane & 31)];
     }
     const S2 sc = qk(ring + (kb % kRingM) * kBlkBytes);
@@ -259,14 +276,30 @@ void sa_mla_kernel(MlaParams p) {
     const uint16_t* kvh = reinterpret_cast<const uint16_t*>(ring + (kb % kRingM) * kBlkBytes);
     const uint16_t* row0 = kvh + (4 * g + (n >> 2)) * (kRowC * 8) + 4 * (n & 3);
     const uint16_t* row1 = row0 + 16 * (kRowC * 8);
-#pragma unroll
-    for (int ct = 0; ct < kCT; ++ct) {
+    // One V^T fragment is read ahead: the two reads of fragment ct+1 are issued
+    // before the two products of fragment ct (the order is pinned below), so the
+    // LDS latency overlaps the matrix work.
+    auto read_v = [&](int ct) {
       const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(row0 + 16 * ct));
       const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(row1 + 16 * ct));
-      const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
-      o[ct] = mfma16x16x32(a, plo, o[ct]);
-      o[ct] = mfma16x16x32(a, phi, o[ct]);
+      return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    bf16x8 a_cur = read_v(0);
+#pragma unroll
+    for (int ct = 0; ct < kCT; ++ct) {
+      bf16x8 a_nxt = a_cur;
+      if (ct + 1 < kCT) a_nxt = read_v(ct + 1);
+      o[ct] = mfma16x16x32(a_cur, plo, o[ct]);
+      o[ct] = mfma16x16x32(a_cur, phi, o[ct]);
+      a_cur = a_nxt;
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int ct = 0; ct < kCT - 1; ++ct) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     vm_cur = vm_next;
   };
 
