@@ -203,8 +203,14 @@ void sa_mla_kernel(MlaParams p) {
 
   static_assert(kRingM == 4, "the waits assume a ring of 4 buffers");
   uint32_t vm_cur = 0u;
-  auto step = [&](const int kb) {
-    uint32_t vm_next = 0u;
+  // The waves of the second half (one of the two waves on each SIMD) meet the
+  // block's barrier after their QK products instead of before them. Every wave
+  // still passes one barrier per block, so barrier kb still orders the copies of
+  // block kb+1 before every read of it and every read of block kb-1 before the
+  // copies that reuse its buffer; the two waves of a SIMD then run half a step
+  // apart, one's QK (LDS-heavy) beside the other's PV (matrix-heavy).
+  const bool late_sync = wis >= (NW + 1) / 2;
+  auto sync_issue = [&](const int kb, uint32_t& vm_next) {
     if (kb + 1 < nb) {
       if (kb + 2 < nb) wait_vmcnt<kUnitsW>();
       else wait_vmcnt<0>();
@@ -217,7 +223,12 @@ void sa_mla_kernel(MlaParams p) {
       vm_next = (uint32_t)__ballot(vslot >= 0);
       vslot = slot[min(kb + 2, nb - 1) * kKB + (lane & 31)];
     }
+  };
+  auto step = [&](const int kb) {
+    uint32_t vm_next = 0u;
+    if (!late_sync) sync_issue(kb, vm_next);
     const S2 sc = qk(ring + (kb % kRingM) * kBlkBytes);
+    if (late_sync) sync_issue(kb, vm_next);
     float sv[8];  // keys 4g + r (r < 4) and 16 + 4g + (r - 4)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {

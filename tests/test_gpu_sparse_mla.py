@@ -50,6 +50,7 @@ CASES = [
     (1, 5, 80, 2048, 2048, 3, 0.5, 0.5),
     (1, 6, 128, 40, 1, 4, 0.0, 2.0),
     (1, 12, 112, 500, 200, 5, 0.9, -1.0),
+    (1, 7, 96, 3000, 1500, 6, 0.3, 0.5),
 ]
 
 
