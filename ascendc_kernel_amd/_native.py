@@ -14,7 +14,7 @@ import torch
 
 from . import build as _build
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DSA_SA_AUTO = 0
 DSA_SA_MULTIPLICITY = 1
@@ -27,7 +27,9 @@ EXPORTS = (
     "dsa_abi_version",
     "dsa_strerror",
     "dsa_sparse_attn_fwd",
+    "dsa_sparse_attn_fwd_i64",
     "dsa_sparse_mla_fwd",
+    "dsa_sparse_mla_fwd_i64",
     "dsa_indexer_rope",
     "dsa_indexer_score_topk",
     "dsa_indexer_workspace_bytes",
@@ -67,16 +69,20 @@ def load() -> ctypes.CDLL:
     lib.dsa_abi_version.argtypes = []
     lib.dsa_strerror.restype = ctypes.c_char_p
     lib.dsa_strerror.argtypes = [ctypes.c_int]
-    lib.dsa_sparse_attn_fwd.restype = ctypes.c_int
-    lib.dsa_sparse_attn_fwd.argtypes = [
-        _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-        ctypes.c_float, ctypes.c_int32, _c_vp]
-    lib.dsa_sparse_mla_fwd.restype = ctypes.c_int
-    lib.dsa_sparse_mla_fwd.argtypes = [
-        _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-        ctypes.c_float, _c_vp]
+    for name in ("dsa_sparse_attn_fwd", "dsa_sparse_attn_fwd_i64"):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [
+            _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+            ctypes.c_float, ctypes.c_int32, _c_vp]
+    for name in ("dsa_sparse_mla_fwd", "dsa_sparse_mla_fwd_i64"):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [
+            _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+            ctypes.c_float, _c_vp]
     lib.dsa_indexer_rope.restype = ctypes.c_int
     lib.dsa_indexer_rope.argtypes = [
         _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32, _c_vp]
@@ -144,13 +150,14 @@ def sparse_attn_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
     dev = _require_gpu(q, kv, topk_idxs)
     q = q.contiguous()
     kv = kv.contiguous()
-    idx = topk_idxs.to(torch.int32).contiguous() if topk_idxs.dtype != torch.int32 else topk_idxs.contiguous()
+    idx = topk_idxs.contiguous()  # int64 indices are read as they are (no narrowing pass)
+    fn = "dsa_sparse_attn_fwd_i64" if idx.dtype == torch.int64 else "dsa_sparse_attn_fwd"
     sink = attn_sink.detach().to(device=dev, dtype=torch.float32).contiguous()
     out = torch.empty_like(q)
-    rc = lib.dsa_sparse_attn_fwd(
+    rc = getattr(lib, fn)(
         q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), out.data_ptr(),
         b, m, h, d, kv.shape[1], idx.shape[2], float(softmax_scale), int(variant), _stream(q))
-    _check("dsa_sparse_attn_fwd", rc)
+    _check(fn, rc)
     return out
 
 
@@ -174,13 +181,14 @@ def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
     dev = _require_gpu(q, kv, topk_idxs)
     q = q.contiguous()
     kv = kv.contiguous()
-    idx = topk_idxs.to(torch.int32).contiguous() if topk_idxs.dtype != torch.int32 else topk_idxs.contiguous()
+    idx = topk_idxs.contiguous()  # int64 indices are read as they are (no narrowing pass)
+    fn = "dsa_sparse_mla_fwd_i64" if idx.dtype == torch.int64 else "dsa_sparse_mla_fwd"
     sink = attn_sink.detach().to(device=dev, dtype=torch.float32).contiguous()
     out = torch.empty(b, m, h, v_dim, dtype=torch.bfloat16, device=dev)
-    rc = lib.dsa_sparse_mla_fwd(
+    rc = getattr(lib, fn)(
         q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), out.data_ptr(),
         b, m, h, dqk, v_dim, kv.shape[2], kv.shape[1], idx.shape[2], float(softmax_scale), _stream(q))
-    _check("dsa_sparse_mla_fwd", rc)
+    _check(fn, rc)
     return out
 
 

@@ -48,6 +48,15 @@ __device__ __forceinline__ void st_nt(T* p, T v) {
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// A topk slot index as int: int32 indices as stored (the kernels mask values < 0
+// and >= n_kv); int64 indices (the indexer's output dtype) narrowed in the kernel,
+// every value outside [0, 2^31) becoming -1 (masked) instead of wrapping.
+__device__ __forceinline__ int slot_index(const int32_t* p, int64_t i) { return p[i]; }
+__device__ __forceinline__ int slot_index(const int64_t* p, int64_t i) {
+  const int64_t v = p[i];
+  return (v >= 0 && v <= INT32_MAX) ? (int)v : -1;
+}
+
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
 // vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14).
 template <int N>

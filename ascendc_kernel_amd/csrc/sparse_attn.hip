@@ -42,7 +42,7 @@ constexpr int kD = 128;
 struct MultParams {
   const uint16_t* q;
   const uint16_t* kv;
-  const int32_t* idx;
+  const void* idx;           // [B, M, TOPK] int32 or int64 (the kernel's IdxT)
   const float* sink;
   uint16_t* out;
   int64_t M;                 // tokens per batch
@@ -92,8 +92,9 @@ __device__ __forceinline__ bf16x8 load_row16(const uint16_t* p) {
 // Four resident workgroups per CU (<= 128 VGPRs, 32 KB LDS each): with two tiles
 // per wave that keeps 128 KB of q loads in flight per CU, which measured faster
 // than three workgroups of four tiles per wave.
-template <int TPW, bool BIGK>
+template <int TPW, bool BIGK, typename IdxT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void sa_mult_kernel(MultParams p) {
+  const IdxT* const idx = static_cast<const IdxT*>(p.idx);
   __shared__ u32x4 kraw[32 * 16];  // kv row r chunk c (8 channels) at r*16 + (c ^ (r & 15))
   __shared__ u32x4 img_pv[8][64];  // fragment mt: kv[pi(8g+j)][delta(mt, n)], j = 0..7
   __shared__ u32x4 obuf[4][256];   // per-wave output tile, 16 rows x 16 chunks, chunk ^ row
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   for (int i = 0; i < TPW; ++i) {
     skv[i] = p.sink[h0[i] + n];
     const int64_t tj = tok[0] + i < tok_last ? tok[0] + i : tok_last;
-    idxv[i] = p.idx[tj * p.TOPK + (lane < p.TOPK ? lane : p.TOPK - 1)];
+    idxv[i] = slot_index(idx, tj * p.TOPK + (lane < p.TOPK ? lane : p.TOPK - 1));
   }
   __builtin_amdgcn_sched_barrier(0);
   // 2. q loads of all this wave's tiles.
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
           for (int q = 0; q < TPW; ++q)
             if (q == jt && lane < p.TOPK) v = idxv[q];
         } else if (c0 + lane < p.TOPK) {  // only for topk > 64
-          v = p.idx[tok[i] * p.TOPK + c0 + lane];
+          v = slot_index(idx, tok[i] * p.TOPK + c0 + lane);
         }
         if (v >= p.NKV) v = -1;  // out-of-range slots are ignored (masked)
 #pragma unroll
@@ -337,14 +338,16 @@ extern "C" const char* dsa_strerror(int code) {
   }
 }
 
-int dsa_sparse_attn_gather_launch(const void* q, const void* kv, const int32_t* idx, const float* sink,
-                                  void* out, int64_t b, int64_t m, int64_t h, int64_t n_kv,
-                                  int64_t topk, float scale, hipStream_t stream);
+int dsa_sparse_attn_gather_launch(const void* q, const void* kv, const void* idx, bool idx64,
+                                  const float* sink, void* out, int64_t b, int64_t m, int64_t h,
+                                  int64_t n_kv, int64_t topk, float scale, hipStream_t stream);
 
-extern "C" int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
-                                   const float* attn_sink, void* out, int64_t b, int64_t m,
-                                   int64_t h, int64_t d, int64_t n_kv, int64_t topk,
-                                   float softmax_scale, int32_t variant, void* stream) {
+namespace {
+
+// Shared by dsa_sparse_attn_fwd (int32 indices) and dsa_sparse_attn_fwd_i64.
+int sparse_attn_fwd(const void* q, const void* kv, const void* topk_idxs, bool idx64,
+                    const float* attn_sink, void* out, int64_t b, int64_t m, int64_t h, int64_t d,
+                    int64_t n_kv, int64_t topk, float softmax_scale, int32_t variant, void* stream) {
   if (b < 0 || m < 0 || h <= 0 || d <= 0 || n_kv < 1 || topk < 1) return DSA_ERR_SHAPE;
   if (d != kD || (h % 16) != 0) return DSA_ERR_UNSUPPORTED;
   if (variant == DSA_SA_AUTO) variant = (n_kv <= 32) ? DSA_SA_MULTIPLICITY : DSA_SA_GATHER;
@@ -359,8 +362,8 @@ extern "C" int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t*
     return DSA_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
   if (variant == DSA_SA_GATHER)
-    return dsa_sparse_attn_gather_launch(q, kv, topk_idxs, attn_sink, out, b, m, h, n_kv, topk,
-                                         softmax_scale, s);
+    return dsa_sparse_attn_gather_launch(q, kv, topk_idxs, idx64, attn_sink, out, b, m, h, n_kv,
+                                         topk, softmax_scale, s);
 
   MultParams p;
   p.q = (const uint16_t*)q;
@@ -378,9 +381,35 @@ extern "C" int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t*
   p.blocks_per_batch = (p.tiles_per_batch + tiles_per_block - 1) / tiles_per_block;
   const int64_t blocks = b * p.blocks_per_batch;
   if (blocks > INT32_MAX) return DSA_ERR_SHAPE;
-  if (topk <= 64)
-    hipLaunchKernelGGL((sa_mult_kernel<DSA_SA_TILES_PER_WAVE, false>), dim3((unsigned)blocks), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((sa_mult_kernel<DSA_SA_TILES_PER_WAVE, true>), dim3((unsigned)blocks), dim3(256), 0, s, p);
+  const dim3 grid((unsigned)blocks);
+  if (idx64) {
+    if (topk <= 64)
+      hipLaunchKernelGGL((sa_mult_kernel<DSA_SA_TILES_PER_WAVE, false, int64_t>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((sa_mult_kernel<DSA_SA_TILES_PER_WAVE, true, int64_t>), grid, dim3(256), 0, s, p);
+  } else {
+    if (topk <= 64)
+      hipLaunchKernelGGL((sa_mult_kernel<DSA_SA_TILES_PER_WAVE, false, int32_t>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((sa_mult_kernel<DSA_SA_TILES_PER_WAVE, true, int32_t>), grid, dim3(256), 0, s, p);
+  }
   return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
+                                   const float* attn_sink, void* out, int64_t b, int64_t m,
+                                   int64_t h, int64_t d, int64_t n_kv, int64_t topk,
+                                   float softmax_scale, int32_t variant, void* stream) {
+  return sparse_attn_fwd(q, kv, topk_idxs, false, attn_sink, out, b, m, h, d, n_kv, topk,
+                         softmax_scale, variant, stream);
+}
+
+extern "C" int dsa_sparse_attn_fwd_i64(const void* q, const void* kv, const int64_t* topk_idxs,
+                                       const float* attn_sink, void* out, int64_t b, int64_t m,
+                                       int64_t h, int64_t d, int64_t n_kv, int64_t topk,
+                                       float softmax_scale, int32_t variant, void* stream) {
+  return sparse_attn_fwd(q, kv, topk_idxs, true, attn_sink, out, b, m, h, d, n_kv, topk,
+                         softmax_scale, variant, stream);
 }

@@ -40,7 +40,7 @@ typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 struct GatherParams {
   const uint16_t* q;     // [B, M, H, 128]
   const uint16_t* kv;    // [B, NKV, 128]
-  const int32_t* idx;    // [B, M, TOPK]
+  const void* idx;       // [B, M, TOPK] int32 or int64 (the kernel's IdxT)
   const float* sink;     // [H]
   uint16_t* out;         // [B, M, H, 128]
   int64_t M;
@@ -59,9 +59,10 @@ __device__ __forceinline__ int out_ch(int dt, int i) {
 // LDS row r (256 B = 16 chunks of 16 B): chunk c lives at r*16 + (c ^ (r & 15)).
 __device__ __forceinline__ int swz(int r, int c) { return r * 16 + (c ^ (r & 15)); }
 
-template <int NW>
+template <int NW, typename IdxT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW >= 2 ? 2 : 1)))
 void sa_gather_kernel(GatherParams p) {
+  const IdxT* const idx = static_cast<const IdxT*>(p.idx);
   __shared__ u32x4 ring[kRing][kKB * 16];  // kRing blocks of 32 gathered rows (8 KB each)
   __shared__ int32_t nblk_w[NW];  // per wave: blocks up to its last valid slot
   extern __shared__ int32_t slot[];         // the token's slot indices (masked -> -1)
@@ -112,7 +113,7 @@ void sa_gather_kernel(GatherParams p) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int s = s0 + 64 * NW * u + tid;
-      v[u] = p.idx[tok * p.TOPK + min(s, p.TOPK - 1)];  // unconditional (see q)
+      v[u] = slot_index(idx, tok * p.TOPK + min(s, p.TOPK - 1));  // unconditional (see q)
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -378,9 +379,9 @@ void sa_gather_kernel(GatherParams p) {
 
 }  // namespace
 
-int dsa_sparse_attn_gather_launch(const void* q, const void* kv, const int32_t* idx, const float* sink,
-                                  void* out, int64_t b, int64_t m, int64_t h, int64_t n_kv,
-                                  int64_t topk, float scale, hipStream_t stream) {
+int dsa_sparse_attn_gather_launch(const void* q, const void* kv, const void* idx, bool idx64,
+                                  const float* sink, void* out, int64_t b, int64_t m, int64_t h,
+                                  int64_t n_kv, int64_t topk, float scale, hipStream_t stream) {
   if (h % 16 != 0 || h > 128) return DSA_ERR_UNSUPPORTED;
   if (topk > 2048) return DSA_ERR_UNSUPPORTED;
   if (!(scale > 0.f) || !(scale < INFINITY)) return DSA_ERR_UNSUPPORTED;  // the kernel's max uses scale > 0
@@ -403,12 +404,22 @@ int dsa_sparse_attn_gather_launch(const void* q, const void* kv, const int32_t* 
   const dim3 grid((unsigned)tokens);
   // Dynamic LDS: the slot list, padded to whole blocks.
   const size_t smem = (size_t)((topk + kKB - 1) / kKB) * kKB * sizeof(int32_t);
-  switch ((h + 31) / 32) {
-    case 1: hipLaunchKernelGGL(sa_gather_kernel<1>, grid, dim3(64), smem, stream, p); break;
-    case 2: hipLaunchKernelGGL(sa_gather_kernel<2>, grid, dim3(128), smem, stream, p); break;
-    case 3: hipLaunchKernelGGL(sa_gather_kernel<3>, grid, dim3(192), smem, stream, p); break;
-    case 4: hipLaunchKernelGGL(sa_gather_kernel<4>, grid, dim3(256), smem, stream, p); break;
-    default: return DSA_ERR_UNSUPPORTED;
+  const int nw = (int)((h + 31) / 32);
+  if (nw < 1 || nw > 4) return DSA_ERR_UNSUPPORTED;
+  if (idx64) {
+    switch (nw) {
+      case 1: hipLaunchKernelGGL((sa_gather_kernel<1, int64_t>), grid, dim3(64), smem, stream, p); break;
+      case 2: hipLaunchKernelGGL((sa_gather_kernel<2, int64_t>), grid, dim3(128), smem, stream, p); break;
+      case 3: hipLaunchKernelGGL((sa_gather_kernel<3, int64_t>), grid, dim3(192), smem, stream, p); break;
+      default: hipLaunchKernelGGL((sa_gather_kernel<4, int64_t>), grid, dim3(256), smem, stream, p); break;
+    }
+  } else {
+    switch (nw) {
+      case 1: hipLaunchKernelGGL((sa_gather_kernel<1, int32_t>), grid, dim3(64), smem, stream, p); break;
+      case 2: hipLaunchKernelGGL((sa_gather_kernel<2, int32_t>), grid, dim3(128), smem, stream, p); break;
+      case 3: hipLaunchKernelGGL((sa_gather_kernel<3, int32_t>), grid, dim3(192), smem, stream, p); break;
+      default: hipLaunchKernelGGL((sa_gather_kernel<4, int32_t>), grid, dim3(256), smem, stream, p); break;
+    }
   }
   return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
 }

@@ -44,7 +44,7 @@ typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 struct MlaParams {
   const uint16_t* q;     // [B, M, H, 576]
   const uint16_t* kv;    // [B, NKV, kv_dim] (kv_dim >= 576 channels per row)
-  const int32_t* idx;    // [B, M, TOPK]
+  const void* idx;       // [B, M, TOPK] int32 or int64 (the kernel's IdxT)
   const float* sink;     // [H]
   uint16_t* out;         // [B, M, H, 512]
   int64_t M;
@@ -56,9 +56,10 @@ struct S2 {
   f32x4 t0, t1;
 };
 
-template <int NW>
+template <int NW, typename IdxT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sa_mla_kernel(MlaParams p) {
+  const IdxT* const idx = static_cast<const IdxT*>(p.idx);
   extern __shared__ __align__(16) uint8_t smem[];
   uint8_t* ring = smem;                                                   // [kRingM][kBlkBytes]
   int32_t* slot = reinterpret_cast<int32_t*>(smem + kRingM * kBlkBytes);  // [nblk * 32]
@@ -93,7 +94,7 @@ void sa_mla_kernel(MlaParams p) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int s = s0 + 64 * NW * u + tid;
-      v[u] = p.idx[tok * p.TOPK + min(s, p.TOPK - 1)];
+      v[u] = slot_index(idx, tok * p.TOPK + min(s, p.TOPK - 1));
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -347,12 +348,34 @@ void sa_mla_kernel(MlaParams p) {
       st_nt(dst + r * 64 + lane, *reinterpret_cast<const u32x4*>(obuf + r * 1024 + (lane ^ r) * 16));
 }
 
-}  // namespace
+template <typename IdxT>
+int mla_launch(const MlaParams& p, int nw, size_t smem, hipStream_t st) {
+  const dim3 grid((unsigned)((int64_t)p.B * p.M));
+  switch (nw) {
+#define DSA_MLA_CASE(n)                                                                           \
+  case n:                                                                                         \
+    if (hipFuncSetAttribute((const void*)sa_mla_kernel<n, IdxT>,                                   \
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)   \
+      return DSA_ERR_LAUNCH;                                                                      \
+    hipLaunchKernelGGL((sa_mla_kernel<n, IdxT>), grid, dim3(64 * n), smem, st, p);                \
+    break;
+    DSA_MLA_CASE(4)
+    DSA_MLA_CASE(5)
+    DSA_MLA_CASE(6)
+    DSA_MLA_CASE(7)
+    DSA_MLA_CASE(8)
+#undef DSA_MLA_CASE
+    default:
+      return DSA_ERR_UNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+}
 
-extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
-                                  const float* attn_sink, void* out, int64_t b, int64_t m,
-                                  int64_t h, int64_t d_qk, int64_t d_v, int64_t kv_dim,
-                                  int64_t n_kv, int64_t topk, float softmax_scale, void* stream) {
+// Shared by dsa_sparse_mla_fwd (int32 indices) and dsa_sparse_mla_fwd_i64.
+int sparse_mla_fwd(const void* q, const void* kv, const void* topk_idxs, bool idx64,
+                   const float* attn_sink, void* out, int64_t b, int64_t m, int64_t h,
+                   int64_t d_qk, int64_t d_v, int64_t kv_dim, int64_t n_kv, int64_t topk,
+                   float softmax_scale, void* stream) {
   if (b < 0 || m < 0 || h <= 0 || n_kv < 1 || topk < 1) return DSA_ERR_SHAPE;
   if (d_qk != kDQK || d_v != kDV || kv_dim < kDQK) return DSA_ERR_UNSUPPORTED;
   // 4..8 waves of 16 heads (with fewer, a block takes too many copies per wave to
@@ -380,23 +403,25 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
   const int64_t nblk = (topk + kKB - 1) / kKB;
   const size_t smem = (size_t)kRingM * kBlkBytes + (size_t)nblk * kKB * 4 + 32;  // + per-wave counts
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)(b * m));
-  switch (h / 16) {
-#define DSA_MLA_CASE(nw)                                                                          \
-  case nw:                                                                                        \
-    if (hipFuncSetAttribute((const void*)sa_mla_kernel<nw>,                                        \
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)   \
-      return DSA_ERR_LAUNCH;                                                                      \
-    hipLaunchKernelGGL(sa_mla_kernel<nw>, grid, dim3(64 * nw), smem, st, p);                      \
-    break;
-    DSA_MLA_CASE(4)
-    DSA_MLA_CASE(5)
-    DSA_MLA_CASE(6)
-    DSA_MLA_CASE(7)
-    DSA_MLA_CASE(8)
-#undef DSA_MLA_CASE
-    default:
-      return DSA_ERR_UNSUPPORTED;
-  }
-  return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+  return idx64 ? mla_launch<int64_t>(p, (int)(h / 16), smem, st)
+               : mla_launch<int32_t>(p, (int)(h / 16), smem, st);
+}
+
+}  // namespace
+
+extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
+                                  const float* attn_sink, void* out, int64_t b, int64_t m,
+                                  int64_t h, int64_t d_qk, int64_t d_v, int64_t kv_dim,
+                                  int64_t n_kv, int64_t topk, float softmax_scale, void* stream) {
+  return sparse_mla_fwd(q, kv, topk_idxs, false, attn_sink, out, b, m, h, d_qk, d_v, kv_dim, n_kv,
+                        topk, softmax_scale, stream);
+}
+
+extern "C" int dsa_sparse_mla_fwd_i64(const void* q, const void* kv, const int64_t* topk_idxs,
+                                      const float* attn_sink, void* out, int64_t b, int64_t m,
+                                      int64_t h, int64_t d_qk, int64_t d_v, int64_t kv_dim,
+                                      int64_t n_kv, int64_t topk, float softmax_scale,
+                                      void* stream) {
+  return sparse_mla_fwd(q, kv, topk_idxs, true, attn_sink, out, b, m, h, d_qk, d_v, kv_dim, n_kv,
+                        topk, softmax_scale, stream);
 }

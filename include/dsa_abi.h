@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 1
+#define DSA_ABI_VERSION 2
 
 #define DSA_OK 0
 #define DSA_ERR_NULL (-1)        /* a required pointer is NULL */
@@ -74,6 +74,18 @@ int dsa_sparse_attn_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
                         float softmax_scale, int32_t variant, void* stream);
 
 /*
+ * dsa_sparse_attn_fwd with int64 topk_idxs, the dtype the indexer returns
+ * (reference/task2_v0_ref.py:138-143) and sparse_attn_ref accepts as well
+ * (task1_v0_ref.py:8-12 indexes with whatever integer tensor it is given). The
+ * kernels read the int64 values themselves (no narrowing pass); a value outside
+ * [0, n_kv), including any outside the int32 range, is a masked slot.
+ */
+int dsa_sparse_attn_fwd_i64(const void* q, const void* kv, const int64_t* topk_idxs,
+                            const float* attn_sink, void* out, int64_t b, int64_t m,
+                            int64_t h, int64_t d, int64_t n_kv, int64_t topk,
+                            float softmax_scale, int32_t variant, void* stream);
+
+/*
  * Sparse MLA: Task1 with a key wider than the value (the attention of the DSA layer,
  * configs[4]): one latent kv row is the key (its first d_qk channels) and the value
  * (its first d_v channels):
@@ -94,6 +106,16 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
                        const float* attn_sink, void* out, int64_t b, int64_t m, int64_t h,
                        int64_t d_qk, int64_t d_v, int64_t kv_dim, int64_t n_kv, int64_t topk,
                        float softmax_scale, void* stream);
+
+/*
+ * dsa_sparse_mla_fwd with int64 topk_idxs: the indexer's output (reference/
+ * task2_v0_ref.py:138-143, -1 for masked picks) fed to the attention as it is.
+ * Values outside [0, n_kv) are masked slots.
+ */
+int dsa_sparse_mla_fwd_i64(const void* q, const void* kv, const int64_t* topk_idxs,
+                           const float* attn_sink, void* out, int64_t b, int64_t m, int64_t h,
+                           int64_t d_qk, int64_t d_v, int64_t kv_dim, int64_t n_kv, int64_t topk,
+                           float softmax_scale, void* stream);
 
 /*
  * Task2 RoPE, in place on the last `rd` channels of every head of q.

@@ -131,6 +131,29 @@ def test_sparse_mla_host_checks():
     assert _mla(lib, kv=24) == -6
 
 
+def test_int64_index_entry_points_host_checks():
+    """dsa_sparse_attn_fwd_i64 / dsa_sparse_mla_fwd_i64 share the int32 entry points'
+    checks (they differ only in how the kernels read topk_idxs)."""
+    lib = _native.load()
+    a = [16, 16, 16, 16, 16, 1, 1, 64, 128, 32, 16, 0.1, 0, None]
+    f = lib.dsa_sparse_attn_fwd_i64
+    assert f(*a[:5], -1, *a[6:]) == -2                   # b < 0
+    assert f(*a[:8], 64, *a[9:]) == -3                   # d != 128
+    assert f(*a[:12], 7, None) == -3                     # unknown variant
+    assert f(*a[:9], 33, *a[10:12], 1, None) == -3       # multiplicity variant needs n_kv <= 32
+    assert f(*a[:5], 0, *a[6:]) == 0                     # empty batch: nothing to do
+    assert f(None, *a[1:]) == -1
+    assert f(8, *a[1:]) == -6
+    m = [16, 16, 16, 16, 16, 1, 1, 128, 576, 512, 576, 100, 64, 576 ** -0.5, None]
+    g = lib.dsa_sparse_mla_fwd_i64
+    assert g(*m[:5], -1, *m[6:]) == -2
+    assert g(*m[:8], 512, *m[9:]) == -3                  # d_qk != 576
+    assert g(*m[:12], 2049, *m[13:]) == -3               # topk > 2048
+    assert g(*m[:6], 0, *m[7:]) == 0
+    assert g(*m[:2], None, *m[3:]) == -1                 # no topk_idxs
+    assert g(*m[:4], None, *m[5:]) == -1                 # no out
+
+
 def _ixw(lib, **kw):
     a = dict(q=16, kv=16, kvbs=8192 * 128, wl=16, scale=0.011, fr=16, mode=1, out=16, b=1, s=8,
              h=64, d=128, rd=64, T=8192, K=2048, ratio=1, causal=1, offset=0, ws=16, wsb=1 << 20)

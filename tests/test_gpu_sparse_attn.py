@@ -141,6 +141,29 @@ def test_int64_indices_and_side_stream(gpu):
     _compare(out, ref, "int64-stream")
 
 
+@pytest.mark.parametrize("variant,n_kv,topk", [(_native.DSA_SA_MULTIPLICITY, 32, 16),
+                                                 (_native.DSA_SA_MULTIPLICITY, 32, 100),
+                                                 (_native.DSA_SA_GATHER, 500, 200)])
+def test_int64_indices_read_in_kernel(gpu, variant, n_kv, topk):
+    """int64 indices (dsa_sparse_attn_fwd_i64) give the int32 path's output bit for bit;
+    values outside [0, n_kv), also beyond the int32 range, are masked slots and are
+    not wrapped: 2^32 + 3 must not select row 3."""
+    q, kv, idx, sink = _case(2, 24, 64, n_kv, topk, 14, 0.1, 0.5)
+    _say("case int64 in-kernel", variant, n_kv, topk)
+    i64 = idx.long()
+    big = torch.tensor([2 ** 32 + 3, 2 ** 31, -(2 ** 32) + 5, -7, n_kv + 3, 2 ** 40 + 1],
+                       dtype=torch.int64, device=gpu)
+    sel = torch.rand(idx.shape, generator=torch.Generator().manual_seed(15)) < 0.2
+    fill = big[torch.randint(0, len(big), idx.shape, generator=torch.Generator().manual_seed(16))]
+    i64 = torch.where(sel.to(gpu), fill, i64)
+    i32 = torch.where((i64 >= 0) & (i64 < n_kv), i64, -1).to(torch.int32)
+    out64 = _native.sparse_attn_fwd(q, kv, i64, sink, 128 ** -0.5, variant=variant)
+    out32 = _native.sparse_attn_fwd(q, kv, i32, sink, 128 ** -0.5, variant=variant)
+    assert torch.equal(out64.view(torch.int16), out32.view(torch.int16))
+    ref = osa.sparse_attn_ref(q, kv, sink, i32, 128 ** -0.5)
+    _compare(out64, ref, f"int64-{variant}")
+
+
 def test_fixture_masked_needs_gather_variant(gpu):
     """n_kv = 48 > 32 selects the gather variant."""
     f = np.load(os.path.join(GOLDEN, "task1_masked.npz"))

@@ -76,6 +76,25 @@ def test_mla_masked_tokens_oob_and_wide_rows(gpu):
     assert torch.count_nonzero(out[0, 1]) == 0
 
 
+def test_mla_int64_indices_read_in_kernel(gpu):
+    """int64 indices (dsa_sparse_mla_fwd_i64, the indexer's dtype) give the int32 path's
+    output bit for bit; values outside [0, n_kv), also beyond int32, are masked slots."""
+    q, kv, idx, sink = _case(1, 10, 128, 700, 300, 8, 0.2, 0.5)
+    _say("mla int64 in-kernel")
+    i64 = idx.long()
+    big = torch.tensor([2 ** 32 + 3, 2 ** 31, -(2 ** 32) + 5, 700, 2 ** 40 + 1],
+                       dtype=torch.int64, device=gpu)
+    sel = torch.rand(idx.shape, generator=torch.Generator().manual_seed(17)) < 0.2
+    fill = big[torch.randint(0, len(big), idx.shape, generator=torch.Generator().manual_seed(18))]
+    i64 = torch.where(sel.to(gpu), fill, i64)
+    i32 = torch.where((i64 >= 0) & (i64 < 700), i64, -1).to(torch.int32)
+    out64 = _native.sparse_mla_fwd(q, kv, i64, sink, SCALE, DV)
+    out32 = _native.sparse_mla_fwd(q, kv, i32, sink, SCALE, DV)
+    assert torch.equal(out64.view(torch.int16), out32.view(torch.int16))
+    ref = osa.sparse_attn_ref(q, kv, sink, i32, SCALE, v_dim=DV)
+    _compare(out64, ref, "mla-int64")
+
+
 def test_mla_drop_in_module(gpu):
     """task1 Model with v_dim: the drop-in surface routes to the MLA kernel."""
     q, kv, idx, sink = _case(1, 16, 128, 256, 128, 7, 0.1, 0.0)
