@@ -59,6 +59,8 @@ struct WideParams {
   int32_t B, S, rd, T, K, ratio, causal;
   int64_t offset;
   int32_t groups;       // ceil(S / kTok)
+  int32_t csplit;       // candidate chunks per token group (1 unless the keys go to gkeys)
+  int32_t ctiles;       // candidate tiles per chunk
   int32_t tpad;         // key row length in LDS (T rounded up to 32)
   int32_t psort;        // power of two >= K (pick buffer length)
 };
@@ -352,14 +354,21 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
   const int hf = lane >> 5;
   const int col = lane & 31;
   // Longest causal rows first: the last token groups of every batch start first.
+  // With p.csplit > 1 (few token groups, e.g. decode) a workgroup scores the run of
+  // p.ctiles candidate tiles `chunk` of its group; the tile index n below counts
+  // from that run's first tile nbase.
   const int b = blockIdx.x % p.B;
-  const int grp = p.groups - 1 - (int)(blockIdx.x / p.B);
+  const int rest = (int)(blockIdx.x / p.B);
+  const int chunk = rest % p.csplit;
+  const int grp = p.groups - 1 - rest / p.csplit;
   const int t0 = grp * kTok;
   const int t = t0 + tl;
   const bool tok_ok = t < p.S;
   const int nv = n_valid_w(p, t);
   const int nv_max = n_valid_w(p, min(t0 + kTok - 1, p.S - 1));
-  const int ntiles = (nv_max + kTileC - 1) / kTileC;
+  const int nbase = chunk * p.ctiles;
+  const int ntiles = max(0, min((nv_max + kTileC - 1) / kTileC, nbase + p.ctiles) - nbase);
+  if (!kFused && ntiles == 0 && !p.graw) return;  // a chunk past this group's last tile
   const int64_t row_bt = (int64_t)b * p.S + (tok_ok ? t : 0);
   uint16_t* mykeys = keys + tl * p.tpad;
 
@@ -414,7 +423,7 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
   const uint32_t uoff = 16u * (uint32_t)((lane & 15) ^ (urow & 15));
   const uint32_t ulds = ring_lds + 1024u * (uint32_t)wis;
   auto issue = [&](int n) {
-    lds_dma16(rsrc, (uint32_t)(kTileC * n + urow) * (uint32_t)(kWD * 2) + uoff,
+    lds_dma16(rsrc, (uint32_t)(kTileC * (nbase + n) + urow) * (uint32_t)(kWD * 2) + uoff,
               ulds + 8192u * (uint32_t)(n % kRingW));
   };
 #pragma unroll
@@ -434,7 +443,7 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
       const float tot = t0val + xbuf[((n & 1) * kTok + tl) * kTileC + col];
       uint32_t sc = f2bf(tot);
       if (p.causal) sc = f2bf(bf2f(sc) + 0.0f);  // the reference adds the 0 / -inf mask
-      const int c = kTileC * n + col;
+      const int c = kTileC * (nbase + n) + col;
       if (c < nv) {
         const uint16_t v = (uint16_t)(p.graw ? sc : order_key16(sc));
         if constexpr (kFused) mykeys[c] = v;
@@ -698,6 +707,24 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
   p.causal = causal ? 1 : 0;
   p.offset = offset;
   p.groups = (int32_t)((s + kTok - 1) / kTok);
+  // Candidate split for the two-pass path when the token groups alone would leave
+  // most CUs idle (decode: one group scoring every candidate on one CU): chunks of
+  // at least two tiles, about two workgroups per CU in all.
+  const int64_t ntile_all = (n_cand + kTileC - 1) / kTileC;
+  p.csplit = 1;
+  p.ctiles = (int32_t)(ntile_all > 0 ? ntile_all : 1);
+  if (two_pass) {
+    int cu = 0;
+    if (dsa_host::device_cu_count(&cu) != DSA_OK) return DSA_ERR_DEVICE;
+    const int64_t base = b * (int64_t)p.groups;
+    if (base < 2 * (int64_t)cu && ntile_all >= 4) {
+      int64_t want = (2 * (int64_t)cu + base - 1) / base;
+      if (want > ntile_all / 2) want = ntile_all / 2;
+      const int64_t ct = (ntile_all + want - 1) / want;
+      p.ctiles = (int32_t)ct;
+      p.csplit = (int32_t)((ntile_all + ct - 1) / ct);
+    }
+  }
   int ps = 1;
   while (ps < k_out) ps <<= 1;
   p.psort = ps;
@@ -715,7 +742,7 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
   const void* kfn = fused ? (const void*)ix_wide_kernel<true> : (const void*)ix_wide_kernel<false>;
   if (hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
     return DSA_ERR_LAUNCH;
-  const int64_t blocks = b * p.groups;
+  const int64_t blocks = b * p.groups * (int64_t)p.csplit;
   if (blocks > INT32_MAX || b * s > INT32_MAX) return DSA_ERR_SHAPE;
   if (fused)
     hipLaunchKernelGGL(ix_wide_kernel<true>, dim3((unsigned)blocks), dim3(512), smem, stream, p);

@@ -106,6 +106,11 @@ WIDE = [
     (64, 128, 7, 64, 1),
     (256, 0, 0, 96, 2),
     (4, 8188, 9, 2048, 1),   # decode at the configs[4] size: 4 tokens at the end of 8192
+    # decode shapes take the candidate split (few token groups: each workgroup scores
+    # a run of candidate tiles): one token, 16 tokens (63 chunks of 2 tiles), ratio 2
+    (1, 8191, 2, 2048, 1),
+    (16, 4000, 0, 512, 1),
+    (2, 3006, 1, 256, 2),
 ]
 
 
