@@ -30,6 +30,9 @@ EXPORTS = (
     "dsa_sparse_attn_fwd_i64",
     "dsa_sparse_mla_fwd",
     "dsa_sparse_mla_fwd_i64",
+    "dsa_sparse_mla_workspace_bytes",
+    "dsa_sparse_mla_fwd_ws",
+    "dsa_sparse_mla_fwd_i64_ws",
     "dsa_indexer_rope",
     "dsa_indexer_score_topk",
     "dsa_indexer_workspace_bytes",
@@ -83,6 +86,15 @@ def load() -> ctypes.CDLL:
             _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
             _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
             ctypes.c_float, _c_vp]
+    for name in ("dsa_sparse_mla_fwd_ws", "dsa_sparse_mla_fwd_i64_ws"):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [
+            _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+            ctypes.c_float, _c_vp, _c_i64, _c_vp]
+    lib.dsa_sparse_mla_workspace_bytes.restype = ctypes.c_int64
+    lib.dsa_sparse_mla_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64]
     lib.dsa_indexer_rope.restype = ctypes.c_int
     lib.dsa_indexer_rope.argtypes = [
         _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32, _c_vp]
@@ -162,9 +174,11 @@ def sparse_attn_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
 
 
 def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
-                   attn_sink: torch.Tensor, softmax_scale: float, v_dim: int) -> torch.Tensor:
+                   attn_sink: torch.Tensor, softmax_scale: float, v_dim: int,
+                   split: bool = True) -> torch.Tensor:
     """Sparse MLA on the GPU: q [b,m,h,d_qk], kv [b,n_kv,>=d_qk]; keys are kv[..., :d_qk],
-    values kv[..., :v_dim]; returns bf16 [b,m,h,v_dim]."""
+    values kv[..., :v_dim]; returns bf16 [b,m,h,v_dim]. split=False keeps the one-pass
+    kernel also where the library would split the slot lists (few tokens)."""
     lib = load()
     if q.dim() != 4 or kv.dim() != 3 or topk_idxs.dim() != 3:
         raise ValueError("expected q [b,m,h,d_qk], kv [b,n_kv,kv_dim], topk_idxs [b,m,topk]")
@@ -182,12 +196,20 @@ def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
     q = q.contiguous()
     kv = kv.contiguous()
     idx = topk_idxs.contiguous()  # int64 indices are read as they are (no narrowing pass)
-    fn = "dsa_sparse_mla_fwd_i64" if idx.dtype == torch.int64 else "dsa_sparse_mla_fwd"
     sink = attn_sink.detach().to(device=dev, dtype=torch.float32).contiguous()
     out = torch.empty(b, m, h, v_dim, dtype=torch.bfloat16, device=dev)
-    rc = getattr(lib, fn)(
-        q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), out.data_ptr(),
-        b, m, h, dqk, v_dim, kv.shape[2], kv.shape[1], idx.shape[2], float(softmax_scale), _stream(q))
+    args = (q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), out.data_ptr(),
+            b, m, h, dqk, v_dim, kv.shape[2], kv.shape[1], idx.shape[2], float(softmax_scale))
+    # Few tokens (decode): the slot lists are split over workgroups whose partial
+    # results go to a workspace from torch's caching allocator.
+    ws_bytes = int(lib.dsa_sparse_mla_workspace_bytes(b, m, h, idx.shape[2])) if split else 0
+    if ws_bytes > 0:
+        fn = "dsa_sparse_mla_fwd_i64_ws" if idx.dtype == torch.int64 else "dsa_sparse_mla_fwd_ws"
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        rc = getattr(lib, fn)(*args, ws.data_ptr(), ws_bytes, _stream(q))
+    else:
+        fn = "dsa_sparse_mla_fwd_i64" if idx.dtype == torch.int64 else "dsa_sparse_mla_fwd"
+        rc = getattr(lib, fn)(*args, _stream(q))
     _check(fn, rc)
     return out
 

@@ -48,6 +48,10 @@ struct MlaParams {
   const float* sink;     // [H]
   uint16_t* out;         // [B, M, H, 512]
   int64_t M;
+  float* part;           // split mode: [B*M, nsplit, H, 512] fp32 unnormalised O^T rows ...
+  float* ml;             // ... and [B*M, nsplit, H, 2] (running max, log2 domain; sum); else null
+  int32_t nsplit;        // workgroups per token (1: the whole slot list, bf16 output)
+  int32_t bps;           // slot blocks per split
   int32_t B, H, NKV, TOPK, kv_dim;
   float scale_log2;
 };
@@ -56,7 +60,10 @@ struct S2 {
   f32x4 t0, t1;
 };
 
-template <int NW, typename IdxT>
+// kSplit: the token's slot blocks are divided among p.nsplit workgroups, each
+// writing its unnormalised partial state to p.part / p.ml (a separate
+// instantiation, so the one-pass kernel's code is unchanged by it).
+template <int NW, typename IdxT, bool kSplit>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sa_mla_kernel(MlaParams p) {
   const IdxT* const idx = static_cast<const IdxT*>(p.idx);
@@ -65,11 +72,16 @@ void sa_mla_kernel(MlaParams p) {
   int32_t* slot = reinterpret_cast<int32_t*>(smem + kRingM * kBlkBytes);  // [nblk * 32]
   const int nblk = (p.TOPK + kKB - 1) / kKB;
   int32_t* nblk_sh = slot + nblk * kKB;  // [NW] blocks up to each wave's last valid slot
+  // Split mode: workgroup (token, sp) takes slot blocks [kb0, kb0 + nbl) of the token;
+  // `slot` and the block numbers kb below count from kb0.
+  const int64_t tok = kSplit ? (int64_t)(blockIdx.x / p.nsplit) : (int64_t)blockIdx.x;
+  const int sp = kSplit ? (int)(blockIdx.x % p.nsplit) : 0;
+  const int kb0 = kSplit ? sp * p.bps : 0;
+  const int nbl = kSplit ? max(0, min(p.bps, nblk - kb0)) : nblk;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wi = tid >> 6;
-  const int64_t tok = blockIdx.x;
   const int b = (int)(tok / p.M);
   const int n = lane & 15;  // head 16wi + n
   const int g = lane >> 4;  // lane group: k-slice 8g..8g+7, C rows 4g..4g+3
@@ -93,21 +105,21 @@ void sa_mla_kernel(MlaParams p) {
     int v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int s = s0 + 64 * NW * u + tid;
+      const int s = kb0 * kKB + s0 + 64 * NW * u + tid;
       v[u] = slot_index(idx, tok * p.TOPK + min(s, p.TOPK - 1));
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int s = s0 + 64 * NW * u + tid;
-      if (s < nblk * kKB) {
-        const int w = (s < p.TOPK && v[u] < p.NKV) ? v[u] : -1;
+      if (s < nbl * kKB) {
+        const int w = (kb0 * kKB + s < p.TOPK && v[u] < p.NKV) ? v[u] : -1;
         slot[s] = w;
         if (w >= 0) last = s / kKB + 1;
       }
     }
   };
   slot_chunk(0);
-  for (int s0 = 8 * 64 * NW; s0 < nblk * kKB; s0 += 8 * 64 * NW) slot_chunk(s0);
+  for (int s0 = 8 * 64 * NW; s0 < nbl * kKB; s0 += 8 * 64 * NW) slot_chunk(s0);
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) last = max(last, __shfl_xor(last, m, 64));
   if (lane == 0) nblk_sh[wi] = last;
@@ -329,6 +341,17 @@ void sa_mla_kernel(MlaParams p) {
   // Z = the sum over the 4 lane groups + exp2(sink - m).
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
+  if constexpr (kSplit) {
+    // Split mode: this range's state relative to its running max m_run (the sink is
+    // applied once, by sa_mla_combine_kernel). Lane (n, g) holds channels
+    // 16ct + 4g .. +3 of head 16wi + n.
+    const int64_t prow = (tok * p.nsplit + sp) * p.H + head;
+    float* dstp = p.part + prow * kDV + 4 * g;
+#pragma unroll
+    for (int ct = 0; ct < kCT; ++ct) *reinterpret_cast<f32x4*>(dstp + 16 * ct) = o[ct];
+    if (g == 0) *reinterpret_cast<float2*>(p.ml + prow * 2) = make_float2(m_run, l_run);
+    return;
+  }
   const float rz = 1.0f / (l_run + __builtin_amdgcn_exp2f(sink_l2 - m_run));
   // O^T lane data: head n, channels 16ct + 4g + r. Transpose through LDS: per wave
   // 16 head rows of 64 chunks (1 KB); chunk q of row n sits at n*64 + (q ^ n).
@@ -348,16 +371,74 @@ void sa_mla_kernel(MlaParams p) {
       st_nt(dst + r * 64 + lane, *reinterpret_cast<const u32x4*>(obuf + r * 1024 + (lane ^ r) * 16));
 }
 
-template <typename IdxT>
+// Split mode's second step: per (token, head) row, M = max(sink, m_i),
+// Z = exp2(sink - M) + sum_i l_i exp2(m_i - M), out = bf16(sum_i O_i exp2(m_i - M) / Z).
+// One workgroup of 256 threads per two rows, 4 channels per thread.
+struct MlaCombineParams {
+  const float* part;
+  const float* ml;
+  const float* sink;
+  uint16_t* out;
+  int64_t rows;  // B * M * H
+  int32_t H, nsplit;
+};
+
+__global__ __launch_bounds__(256) void sa_mla_combine_kernel(MlaCombineParams p) {
+  const int64_t row = (int64_t)blockIdx.x * 2 + (threadIdx.x >> 7);
+  if (row >= p.rows) return;
+  const int c4 = threadIdx.x & 127;
+  const int head = (int)(row % p.H);
+  const int64_t tok = row / p.H;
+  const float sink_l2 = p.sink[head] * kLog2e;
+  const int64_t r0 = tok * p.nsplit * p.H + head;  // partial row of split 0
+  float mx = sink_l2;
+  for (int i = 0; i < p.nsplit; ++i) mx = fmaxf(mx, p.ml[(r0 + (int64_t)i * p.H) * 2]);
+  float z = __builtin_amdgcn_exp2f(sink_l2 - mx);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < p.nsplit; ++i) {
+    const int64_t ri = r0 + (int64_t)i * p.H;
+    const float2 ml = *reinterpret_cast<const float2*>(p.ml + ri * 2);
+    const float w = __builtin_amdgcn_exp2f(ml.x - mx);
+    z += ml.y * w;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p.part + ri * kDV + 4 * c4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] += v[r] * w;
+  }
+  const float rz = 1.0f / z;
+  uint2 pk;
+  pk.x = pack_bf2(acc[0] * rz, acc[1] * rz);
+  pk.y = pack_bf2(acc[2] * rz, acc[3] * rz);
+  *reinterpret_cast<uint2*>(p.out + row * kDV + 4 * c4) = pk;
+}
+
+// Split plan: with fewer tokens than CUs, each token's slot blocks are divided
+// among workgroups (at least two blocks each) so about two workgroups per CU run.
+void mla_split_plan(int64_t tokens, int64_t topk, int cu, int* nsplit, int* bps) {
+  const int nblk = (int)((topk + kKB - 1) / kKB);
+  *nsplit = 1;
+  *bps = nblk;
+  if (tokens <= 0 || tokens >= cu || nblk < 4) return;
+  int64_t want = (2 * (int64_t)cu + tokens - 1) / tokens;
+  if (want > nblk / 2) want = nblk / 2;
+  const int per = (int)((nblk + want - 1) / want);
+  *bps = per;
+  *nsplit = (nblk + per - 1) / per;
+}
+
+int64_t mla_split_bytes(int64_t tokens, int64_t h, int nsplit) {
+  return nsplit > 1 ? tokens * nsplit * h * (kDV + 2) * 4 : 0;
+}
+
+template <typename IdxT, bool kSplit>
 int mla_launch(const MlaParams& p, int nw, size_t smem, hipStream_t st) {
-  const dim3 grid((unsigned)((int64_t)p.B * p.M));
+  const dim3 grid((unsigned)((int64_t)p.B * p.M * p.nsplit));
   switch (nw) {
 #define DSA_MLA_CASE(n)                                                                           \
   case n:                                                                                         \
-    if (hipFuncSetAttribute((const void*)sa_mla_kernel<n, IdxT>,                                   \
+    if (hipFuncSetAttribute((const void*)sa_mla_kernel<n, IdxT, kSplit>,                           \
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)   \
       return DSA_ERR_LAUNCH;                                                                      \
-    hipLaunchKernelGGL((sa_mla_kernel<n, IdxT>), grid, dim3(64 * n), smem, st, p);                \
+    hipLaunchKernelGGL((sa_mla_kernel<n, IdxT, kSplit>), grid, dim3(64 * n), smem, st, p);        \
     break;
     DSA_MLA_CASE(4)
     DSA_MLA_CASE(5)
@@ -375,8 +456,8 @@ int mla_launch(const MlaParams& p, int nw, size_t smem, hipStream_t st) {
 int sparse_mla_fwd(const void* q, const void* kv, const void* topk_idxs, bool idx64,
                    const float* attn_sink, void* out, int64_t b, int64_t m, int64_t h,
                    int64_t d_qk, int64_t d_v, int64_t kv_dim, int64_t n_kv, int64_t topk,
-                   float softmax_scale, void* stream) {
-  if (b < 0 || m < 0 || h <= 0 || n_kv < 1 || topk < 1) return DSA_ERR_SHAPE;
+                   float softmax_scale, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (b < 0 || m < 0 || h <= 0 || n_kv < 1 || topk < 1 || workspace_bytes < 0) return DSA_ERR_SHAPE;
   if (d_qk != kDQK || d_v != kDV || kv_dim < kDQK) return DSA_ERR_UNSUPPORTED;
   // 4..8 waves of 16 heads (with fewer, a block takes too many copies per wave to
   // keep two blocks in flight under the 6-bit vmcnt).
@@ -401,10 +482,44 @@ int sparse_mla_fwd(const void* q, const void* kv, const void* topk_idxs, bool id
   p.kv_dim = (int32_t)kv_dim;
   p.scale_log2 = softmax_scale * kLog2e;
   const int64_t nblk = (topk + kKB - 1) / kKB;
+  p.part = nullptr;
+  p.ml = nullptr;
+  p.nsplit = 1;
+  p.bps = (int32_t)nblk;
+  if (workspace != nullptr) {
+    int cu = 0;
+    if (dsa_host::device_cu_count(&cu) != DSA_OK) return DSA_ERR_DEVICE;
+    int nsplit, bps;
+    mla_split_plan(b * m, topk, cu, &nsplit, &bps);
+    const int64_t need = mla_split_bytes(b * m, h, nsplit);
+    if (need > 0 && workspace_bytes >= need) {  // else the one-pass kernel (nothing to split)
+      if (!dsa_host::aligned16(workspace)) return DSA_ERR_ALIGN;
+      if (b * m * nsplit > INT32_MAX) return DSA_ERR_SHAPE;
+      p.part = (float*)workspace;
+      p.ml = p.part + b * m * nsplit * h * kDV;
+      p.nsplit = nsplit;
+      p.bps = bps;
+    }
+  }
   const size_t smem = (size_t)kRingM * kBlkBytes + (size_t)nblk * kKB * 4 + 32;  // + per-wave counts
   hipStream_t st = (hipStream_t)stream;
-  return idx64 ? mla_launch<int64_t>(p, (int)(h / 16), smem, st)
-               : mla_launch<int32_t>(p, (int)(h / 16), smem, st);
+  const int nw = (int)(h / 16);
+  int rc;
+  if (p.nsplit > 1)
+    rc = idx64 ? mla_launch<int64_t, true>(p, nw, smem, st) : mla_launch<int32_t, true>(p, nw, smem, st);
+  else
+    rc = idx64 ? mla_launch<int64_t, false>(p, nw, smem, st) : mla_launch<int32_t, false>(p, nw, smem, st);
+  if (rc != DSA_OK || p.nsplit == 1) return rc;
+  MlaCombineParams c;
+  c.part = p.part;
+  c.ml = p.ml;
+  c.sink = attn_sink;
+  c.out = (uint16_t*)out;
+  c.rows = b * m * h;
+  c.H = (int32_t)h;
+  c.nsplit = p.nsplit;
+  hipLaunchKernelGGL(sa_mla_combine_kernel, dim3((unsigned)((c.rows + 1) / 2)), dim3(256), 0, st, c);
+  return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
 }
 
 }  // namespace
@@ -414,7 +529,7 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
                                   int64_t h, int64_t d_qk, int64_t d_v, int64_t kv_dim,
                                   int64_t n_kv, int64_t topk, float softmax_scale, void* stream) {
   return sparse_mla_fwd(q, kv, topk_idxs, false, attn_sink, out, b, m, h, d_qk, d_v, kv_dim, n_kv,
-                        topk, softmax_scale, stream);
+                        topk, softmax_scale, nullptr, 0, stream);
 }
 
 extern "C" int dsa_sparse_mla_fwd_i64(const void* q, const void* kv, const int64_t* topk_idxs,
@@ -423,5 +538,32 @@ extern "C" int dsa_sparse_mla_fwd_i64(const void* q, const void* kv, const int64
                                       int64_t n_kv, int64_t topk, float softmax_scale,
                                       void* stream) {
   return sparse_mla_fwd(q, kv, topk_idxs, true, attn_sink, out, b, m, h, d_qk, d_v, kv_dim, n_kv,
-                        topk, softmax_scale, stream);
+                        topk, softmax_scale, nullptr, 0, stream);
+}
+
+extern "C" int64_t dsa_sparse_mla_workspace_bytes(int64_t b, int64_t m, int64_t h, int64_t topk) {
+  if (b <= 0 || m <= 0 || h <= 0 || topk <= 0 || b * m > INT32_MAX) return 0;
+  int cu = 0;
+  if (dsa_host::device_cu_count(&cu) != DSA_OK) return 0;
+  int nsplit, bps;
+  mla_split_plan(b * m, topk, cu, &nsplit, &bps);
+  return mla_split_bytes(b * m, h, nsplit);
+}
+
+extern "C" int dsa_sparse_mla_fwd_ws(const void* q, const void* kv, const int32_t* topk_idxs,
+                                     const float* attn_sink, void* out, int64_t b, int64_t m,
+                                     int64_t h, int64_t d_qk, int64_t d_v, int64_t kv_dim,
+                                     int64_t n_kv, int64_t topk, float softmax_scale,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
+  return sparse_mla_fwd(q, kv, topk_idxs, false, attn_sink, out, b, m, h, d_qk, d_v, kv_dim, n_kv,
+                        topk, softmax_scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dsa_sparse_mla_fwd_i64_ws(const void* q, const void* kv, const int64_t* topk_idxs,
+                                         const float* attn_sink, void* out, int64_t b, int64_t m,
+                                         int64_t h, int64_t d_qk, int64_t d_v, int64_t kv_dim,
+                                         int64_t n_kv, int64_t topk, float softmax_scale,
+                                         void* workspace, int64_t workspace_bytes, void* stream) {
+  return sparse_mla_fwd(q, kv, topk_idxs, true, attn_sink, out, b, m, h, d_qk, d_v, kv_dim, n_kv,
+                        topk, softmax_scale, workspace, workspace_bytes, stream);
 }

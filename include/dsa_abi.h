@@ -118,6 +118,36 @@ int dsa_sparse_mla_fwd_i64(const void* q, const void* kv, const int64_t* topk_id
                            float softmax_scale, void* stream);
 
 /*
+ * Workspace bytes for dsa_sparse_mla_fwd_ws / _i64_ws: with fewer tokens (b * m)
+ * than CUs (decode), each token's slot list is split among several workgroups
+ * whose fp32 partial results go to the workspace and are merged by a second
+ * kernel. Returns 0 when no split applies (then the _ws calls run the one-pass
+ * kernel and need no workspace).
+ * Same computation as sparse_attn_ref (reference/task1_v0_ref.py:5-24) with
+ * v_dim 512; the split changes only the fp32 summation order of the softmax sums.
+ */
+int64_t dsa_sparse_mla_workspace_bytes(int64_t b, int64_t m, int64_t h, int64_t topk);
+
+/*
+ * dsa_sparse_mla_fwd (int32 topk_idxs) / dsa_sparse_mla_fwd_i64 (int64) with a
+ * caller-provided device workspace (16-byte aligned) of workspace_bytes: when
+ * workspace_bytes >= dsa_sparse_mla_workspace_bytes(b, m, h, topk) > 0 the slot
+ * list is split as described there; otherwise the one-pass kernel runs. The
+ * workspace may be reused by calls on one stream; calls that overlap on different
+ * streams need their own.
+ */
+int dsa_sparse_mla_fwd_ws(const void* q, const void* kv, const int32_t* topk_idxs,
+                          const float* attn_sink, void* out, int64_t b, int64_t m, int64_t h,
+                          int64_t d_qk, int64_t d_v, int64_t kv_dim, int64_t n_kv, int64_t topk,
+                          float softmax_scale, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+int dsa_sparse_mla_fwd_i64_ws(const void* q, const void* kv, const int64_t* topk_idxs,
+                              const float* attn_sink, void* out, int64_t b, int64_t m, int64_t h,
+                              int64_t d_qk, int64_t d_v, int64_t kv_dim, int64_t n_kv,
+                              int64_t topk, float softmax_scale, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
+/*
  * Task2 RoPE, in place on the last `rd` channels of every head of q.
  * Replaces apply_rotary_emb(q[..., -rd:], freqs_cis) (reference/task2_v0_ref.py:93-104,131)
  * and the Ascend ix_rope launch (src/indexer_kernel_aiv.asc:19-111; src/task2_indexer.py:1117-1130).

@@ -154,6 +154,21 @@ def test_int64_index_entry_points_host_checks():
     assert g(*m[:4], None, *m[5:]) == -1                 # no out
 
 
+def test_sparse_mla_workspace_entry_points_host_checks():
+    """dsa_sparse_mla_fwd_ws / _i64_ws check shapes like dsa_sparse_mla_fwd and reject a
+    negative workspace size; the workspace query is 0 for empty or invalid requests."""
+    lib = _native.load()
+    m = [16, 16, 16, 16, 16, 1, 1, 128, 576, 512, 576, 100, 64, 576 ** -0.5, 16, 1 << 20, None]
+    for f in (lib.dsa_sparse_mla_fwd_ws, lib.dsa_sparse_mla_fwd_i64_ws):
+        assert f(*m[:5], -1, *m[6:]) == -2
+        assert f(*m[:8], 512, *m[9:]) == -3
+        assert f(*m[:15], -1, None) == -2
+        assert f(*m[:6], 0, *m[7:]) == 0
+        assert f(*m[:2], None, *m[3:]) == -1
+    assert lib.dsa_sparse_mla_workspace_bytes(0, 1, 128, 2048) == 0
+    assert lib.dsa_sparse_mla_workspace_bytes(1, 1, 128, 0) == 0
+
+
 def _ixw(lib, **kw):
     a = dict(q=16, kv=16, kvbs=8192 * 128, wl=16, scale=0.011, fr=16, mode=1, out=16, b=1, s=8,
              h=64, d=128, rd=64, T=8192, K=2048, ratio=1, causal=1, offset=0, ws=16, wsb=1 << 20)

@@ -95,6 +95,37 @@ def test_mla_int64_indices_read_in_kernel(gpu):
     _compare(out64, ref, "mla-int64")
 
 
+SPLIT_CASES = [
+    # b, m, h, n_kv, topk, seed, masked, sink: few tokens, so the slot lists are split
+    # over workgroups (dsa_sparse_mla_fwd_ws) and merged by the combine kernel
+    (1, 1, 128, 8192, 2048, 31, 0.0, 0.0),    # decode at the configs[4] size
+    (1, 4, 128, 8192, 2048, 32, 0.1, 1.0),
+    (2, 16, 64, 3000, 300, 33, 0.3, -1.0),    # topk not a multiple of 32, 4 waves
+    (1, 3, 96, 700, 2000, 34, 0.0, 2.0),      # slots beyond n_kv masked in the kernel
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_mla_split_decode(gpu, case):
+    """Split slot lists (decode): within tolerance of the oracle and of the one-pass
+    kernel; a split whose whole slot range is masked contributes nothing."""
+    b, m, h, n_kv, topk, seed, masked, sink_scale = case
+    q, kv, idx, sink = _case(b, m, h, n_kv, topk, seed, masked, sink_scale)
+    if case[4] == 2000:
+        idx[..., 600:] = -1  # the later splits see only masked slots
+    lib = _native.load()
+    assert lib.dsa_sparse_mla_workspace_bytes(b, m, h, topk) > 0, "expected a split plan"
+    _say("mla split case", case)
+    out = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV)
+    one = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV, split=False)
+    i64 = _native.sparse_mla_fwd(q, kv, idx.long(), sink, SCALE, DV)
+    assert torch.equal(out.view(torch.int16), i64.view(torch.int16))
+    ref = osa.sparse_attn_ref(q, kv, sink, idx, SCALE, v_dim=DV)
+    _compare(out, ref, f"split{case}")
+    _compare(one, ref, f"one-pass{case}")
+    _compare(out, one, f"split-vs-one-pass{case}")
+
+
 def test_mla_drop_in_module(gpu):
     """task1 Model with v_dim: the drop-in surface routes to the MLA kernel."""
     q, kv, idx, sink = _case(1, 16, 128, 256, 128, 7, 0.1, 0.0)
