@@ -371,6 +371,11 @@ void sa_mla_kernel(MlaParams p) {
       st_nt(dst + r * 64 + lane, *reinterpret_cast<const u32x4*>(obuf + r * 1024 + (lane ^ r) * 16));
 }
 
+#ifndef DSA_MLA_MIN_BPS
+#define DSA_MLA_MIN_BPS 2  // slot blocks per split at least (2, 4, 8 measured: 2 best)
+#endif
+constexpr int kMaxSplit = 32;  // splits per token at most (the combine keeps them in registers)
+
 // Split mode's second step: per (token, head) row, M = max(sink, m_i),
 // Z = exp2(sink - M) + sum_i l_i exp2(m_i - M), out = bf16(sum_i O_i exp2(m_i - M) / Z).
 // One workgroup of 256 threads per two rows, 4 channels per thread.
@@ -391,18 +396,32 @@ __global__ __launch_bounds__(256) void sa_mla_combine_kernel(MlaCombineParams p)
   const int64_t tok = row / p.H;
   const float sink_l2 = p.sink[head] * kLog2e;
   const int64_t r0 = tok * p.nsplit * p.H + head;  // partial row of split 0
+  // Splits in groups of 8 whose loads are all issued before any is used (the
+  // host caps nsplit at kMaxSplit).
+  float2 ml[kMaxSplit];
+  f32x4 v[kMaxSplit];
+#pragma unroll
+  for (int i = 0; i < kMaxSplit; ++i) {
+    if (i < p.nsplit) {
+      const int64_t ri = r0 + (int64_t)i * p.H;
+      ml[i] = *reinterpret_cast<const float2*>(p.ml + ri * 2);
+      v[i] = *reinterpret_cast<const f32x4*>(p.part + ri * kDV + 4 * c4);
+    }
+  }
   float mx = sink_l2;
-  for (int i = 0; i < p.nsplit; ++i) mx = fmaxf(mx, p.ml[(r0 + (int64_t)i * p.H) * 2]);
+#pragma unroll
+  for (int i = 0; i < kMaxSplit; ++i)
+    if (i < p.nsplit) mx = fmaxf(mx, ml[i].x);
   float z = __builtin_amdgcn_exp2f(sink_l2 - mx);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < p.nsplit; ++i) {
-    const int64_t ri = r0 + (int64_t)i * p.H;
-    const float2 ml = *reinterpret_cast<const float2*>(p.ml + ri * 2);
-    const float w = __builtin_amdgcn_exp2f(ml.x - mx);
-    z += ml.y * w;
-    const f32x4 v = *reinterpret_cast<const f32x4*>(p.part + ri * kDV + 4 * c4);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] += v[r] * w;
+  for (int i = 0; i < kMaxSplit; ++i) {
+    if (i < p.nsplit) {
+      const float w = __builtin_amdgcn_exp2f(ml[i].x - mx);
+      z += ml[i].y * w;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += v[i][r] * w;
+    }
   }
   const float rz = 1.0f / z;
   uint2 pk;
@@ -412,14 +431,16 @@ __global__ __launch_bounds__(256) void sa_mla_combine_kernel(MlaCombineParams p)
 }
 
 // Split plan: with fewer tokens than CUs, each token's slot blocks are divided
-// among workgroups (at least two blocks each) so about two workgroups per CU run.
+// among workgroups (at least DSA_MLA_MIN_BPS blocks each, at most kMaxSplit
+// splits) so up to about two workgroups per CU run.
 void mla_split_plan(int64_t tokens, int64_t topk, int cu, int* nsplit, int* bps) {
   const int nblk = (int)((topk + kKB - 1) / kKB);
   *nsplit = 1;
   *bps = nblk;
-  if (tokens <= 0 || tokens >= cu || nblk < 4) return;
+  if (tokens <= 0 || tokens >= cu || nblk < 2 * DSA_MLA_MIN_BPS) return;
   int64_t want = (2 * (int64_t)cu + tokens - 1) / tokens;
-  if (want > nblk / 2) want = nblk / 2;
+  if (want > nblk / DSA_MLA_MIN_BPS) want = nblk / DSA_MLA_MIN_BPS;
+  if (want > kMaxSplit) want = kMaxSplit;
   const int per = (int)((nblk + want - 1) / want);
   *bps = per;
   *nsplit = (nblk + per - 1) / per;

@@ -95,3 +95,35 @@ def test_dsa_layer_c5_faster_than_torch_path(gpu):
                       reps=3, warm=1)
     print(f"[perf c5 mla, 256 tokens] kernel {k_us:.1f} us, torch path {r_us:.1f} us, x{r_us / k_us:.1f}", flush=True)
     assert k_us < r_us
+
+
+@pytest.mark.parametrize("seqlen", [1, 4])
+def test_dsa_decode_c5_faster_than_torch_path(gpu, seqlen):
+    """Decode at the configs[4] size: `seqlen` new tokens at the end of the 8192-token
+    context (start_pos 8192 - seqlen: no mask). The indexer Model.forward and sparse MLA
+    over the indexer's int64 picks, each against its torch path, eager (host time
+    included on both sides)."""
+    torch.manual_seed(42)
+    init = t2.get_c5_init_inputs(device=gpu)
+    m = t2.Model(*init).to(gpu)
+    r = oix.IndexerRef(*init).to(gpu)
+    r.wq_b.weight.data.copy_(m.wq_b.weight.data)
+    r.weights_proj.weight.data.copy_(m.weights_proj.weight.data)
+    sp = 8192 - seqlen
+    g = torch.Generator().manual_seed(40 + seqlen)
+    x = torch.randn(1, seqlen, 7168, generator=g).to(torch.bfloat16).to(gpu)
+    qr = torch.randn(1, seqlen, 1536, generator=g).to(torch.bfloat16).to(gpu)
+    q = torch.randn(1, seqlen, 128, 576, generator=g).to(torch.bfloat16).to(gpu)
+    kv = torch.randn(1, 8192, 576, generator=g).to(torch.bfloat16).to(gpu)
+    attn = t1.Model(128, 576, v_dim=512).to(gpu)
+    with torch.no_grad():
+        idx = m(x, qr, sp, 0)
+        assert torch.equal(idx, r(x, qr, sp, 0))
+        ki_us = _median_us(lambda: m(x, qr, sp, 0), reps=20)
+        ri_us = _median_us(lambda: r(x, qr, sp, 0), reps=5)
+        ka_us = _median_us(lambda: attn(q, kv, idx), reps=20)
+        ra_us = _median_us(lambda: osa.sparse_attn_ref(q, kv, attn.attn_sink, idx, attn.softmax_scale,
+                                                       v_dim=512), reps=5)
+    print(f"[perf c5 decode s={seqlen}] indexer {ki_us:.1f} us vs torch {ri_us:.1f} us (x{ri_us / ki_us:.1f}); "
+          f"sparse MLA {ka_us:.1f} us vs torch {ra_us:.1f} us (x{ra_us / ka_us:.1f})", flush=True)
+    assert ki_us < ri_us and ka_us < ra_us
