@@ -145,7 +145,7 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(every config fits one MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(every config fits one MI355X)", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -237,6 +237,53 @@ def main():
         }
         del q4, kv4, idx4
 
+    # ---------------- Decode at the configs[4] size (before the prefill legs, so that the
+    # prefill calls stay the last dispatches of their kernels): one DSA step for one new
+    # token at position 8191 (indexer Model.forward, then sparse MLA over its int64
+    # picks: split slot lists + combine), captured in a HIP graph and replayed; the
+    # eager step (host time included) beside it.
+    if not a.no_c5:
+        torch.manual_seed(42)
+        initd = t2.get_c5_init_inputs(device=dev)
+        ixd = t2.Model(*initd).to(dev)
+        gd = torch.Generator().manual_seed(5)
+        with torch.no_grad():
+            for pd in (ixd.wq_b.weight, ixd.weights_proj.weight):
+                pd.copy_((torch.randn(pd.shape, generator=gd) * 0.02).to(torch.bfloat16))
+        mlad = t1.Model(128, 576, v_dim=512).to(dev)
+        gi = torch.Generator().manual_seed(7)
+        xd = torch.randn(1, 1, 7168, generator=gi).to(torch.bfloat16).to(dev)
+        qrd = torch.randn(1, 1, 1536, generator=gi).to(torch.bfloat16).to(dev)
+        qd = torch.randn(1, 1, 128, 576, generator=gi).to(torch.bfloat16).to(dev)
+        kvd = torch.randn(1, 8192, 576, generator=gi).to(torch.bfloat16).to(dev)
+        stepd = lambda: mlad(qd, kvd, ixd(xd, qrd, 8191, 0))
+        nd = max(20, a.steps)
+        with torch.no_grad():
+            side = torch.cuda.Stream(dev)
+            side.wait_stream(stream)
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    stepd()
+            stream.wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                outd = stepd()
+            _warm(torch, graph.replay, 5, 0.1)
+            ms_dg = _events_time(torch, graph.replay, nd, stream)
+            _warm(torch, stepd, 2, 0.05)
+            ms_de = _events_time(torch, stepd, nd, stream)
+            eq = bool(torch.equal(outd.view(torch.int16), stepd().view(torch.int16)))
+        dsa_decode = {
+            "workload": "configs[4] decode: 1 new token at position 8191 of 8192; indexer 64x128 (qr[1,1,1536], "
+                        "x[1,1,7168], kv_cache[1,8192,128], top-2048, no mask) then sparse MLA q[1,1,128,576] over "
+                        "latent kv[1,8192,576] with the indexer's int64 picks",
+            "graph_us_per_step": round(ms_dg * 1e3, 1),
+            "eager_us_per_step": round(ms_de * 1e3, 1),
+            "graph_replay_equals_eager": eq,
+        }
+        del graph, outd, xd, qrd, qd, kvd, ixd, mlad
+        torch.cuda.empty_cache()
+
     # ---------------- DSA layer: wide indexer + sparse MLA
     if not a.no_c5:
         torch.cuda.empty_cache()
@@ -270,6 +317,7 @@ def main():
         flop_m = valid_m * 128 * (576 + 512) * 2
         bytes_m = qm.numel() * 2 + 8192 * 128 * 512 * 2 + kvm.numel() * 2 + idxm.numel() * 4 + 128 * 4
         score_flop5 = 2 * 64 * 128 * (8192 * 8193 // 2)
+        result["dsa_decode_c5"] = dsa_decode
         result["dsa_layer_c5"] = {
             "workload": "configs[4]: indexer 64x128 from qr[1,8192,1536] / x[1,8192,7168], kv_cache[1,8192,128], "
                         "causal top-2048 (ratio 1, rope_head_dim 64, W ~ N(0,0.02)); sparse MLA q[1,8192,128,576], "
