@@ -139,7 +139,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-task2", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the configs[3] true-gather leg")
-    ap.add_argument("--no-c5", action="store_true", help="skip the configs[4] DSA-layer leg")
+    ap.add_argument("--no-c5", action="store_true", help="skip the configs[4] DSA-layer (prefill) leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the configs[4] decode leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run 5 plain device copies of 256 MiB (counter calibration for rocprofv3 --pmc)")
     a = ap.parse_args()
@@ -242,7 +243,7 @@ def main():
     # token at position 8191 (indexer Model.forward, then sparse MLA over its int64
     # picks: split slot lists + combine), captured in a HIP graph and replayed; the
     # eager step (host time included) beside it.
-    if not a.no_c5:
+    if not a.no_decode:
         torch.manual_seed(42)
         initd = t2.get_c5_init_inputs(device=dev)
         ixd = t2.Model(*initd).to(dev)
@@ -317,7 +318,6 @@ def main():
         flop_m = valid_m * 128 * (576 + 512) * 2
         bytes_m = qm.numel() * 2 + 8192 * 128 * 512 * 2 + kvm.numel() * 2 + idxm.numel() * 4 + 128 * 4
         score_flop5 = 2 * 64 * 128 * (8192 * 8193 // 2)
-        result["dsa_decode_c5"] = dsa_decode
         result["dsa_layer_c5"] = {
             "workload": "configs[4]: indexer 64x128 from qr[1,8192,1536] / x[1,8192,7168], kv_cache[1,8192,128], "
                         "causal top-2048 (ratio 1, rope_head_dim 64, W ~ N(0,0.02)); sparse MLA q[1,8192,128,576], "
@@ -371,6 +371,8 @@ def main():
             "fused_kernel_traffic": _traffic("ix_score_topk_kernel"),
         }
 
+    if not a.no_decode:
+        result["dsa_decode_c5"] = dsa_decode
     if not a.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)
