@@ -203,6 +203,8 @@ def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
     # Few tokens (decode): the slot lists are split over workgroups whose partial
     # results go to a workspace from torch's caching allocator.
     ws_bytes = int(lib.dsa_sparse_mla_workspace_bytes(b, m, h, idx.shape[2])) if split else 0
+    if ws_bytes < 0:
+        _check("dsa_sparse_mla_workspace_bytes", ws_bytes)
     if ws_bytes > 0:
         fn = "dsa_sparse_mla_fwd_i64_ws" if idx.dtype == torch.int64 else "dsa_sparse_mla_fwd_ws"
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -265,6 +267,8 @@ def indexer_score_topk(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor
     _require_gpu(q, kv_cache, wl, *([fr] if fr is not None else []))
     out = torch.empty(b, s, k_out, dtype=torch.int64, device=q.device)
     ws_bytes = int(lib.dsa_indexer_workspace_bytes(b, s, h, d, n_cand)) if use_workspace else 0
+    if ws_bytes < 0:
+        _check("dsa_indexer_workspace_bytes", ws_bytes)
     if ws_bytes > 0:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
         rc = lib.dsa_indexer_score_topk_ws(

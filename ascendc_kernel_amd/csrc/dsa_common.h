@@ -124,8 +124,12 @@ __device__ __forceinline__ void rope_pair(float a, float b, float c, float d, in
 
 }  // namespace dsa
 
-// Host helpers shared by the entry points.
+// Host helpers shared by the entry points. The library's only state: the CU
+// count of each device and the dynamic-LDS limits already set per kernel,
+// both filled on first use and safe to call from several threads.
 namespace dsa_host {
-int device_cu_count(int* out);  // cached per device
+constexpr int kMaxDevices = 64;
+int device_cu_count(int* out);
+int ensure_dyn_lds(const void* fn, int bytes);
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 }  // namespace dsa_host

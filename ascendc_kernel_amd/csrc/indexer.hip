@@ -582,7 +582,8 @@ extern "C" int dsa_indexer_score_topk(const void* q, const void* kv_cache, int64
 
 extern "C" int64_t dsa_indexer_workspace_bytes(int64_t b, int64_t s, int64_t h, int64_t d,
                                                int64_t n_cand) {
-  if (b < 0 || s < 0 || n_cand < 0) return -1;
+  if (b < 0 || s < 0 || n_cand < 0 || b > (1 << 20) || s > (1 << 24) || n_cand > (1 << 24))
+    return DSA_ERR_SHAPE;
   if (h == 64 && d == 128) return dsa_indexer_wide_workspace_bytes(b, s, n_cand);
   return 0;
 }

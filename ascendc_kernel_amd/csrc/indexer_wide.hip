@@ -740,8 +740,7 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
   if (smem > 160 * 1024) return DSA_ERR_UNSUPPORTED;
   const bool fused = p.gkeys == nullptr;
   const void* kfn = fused ? (const void*)ix_wide_kernel<true> : (const void*)ix_wide_kernel<false>;
-  if (hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
-    return DSA_ERR_LAUNCH;
+  if (dsa_host::ensure_dyn_lds(kfn, (int)smem) != DSA_OK) return DSA_ERR_LAUNCH;
   const int64_t blocks = b * p.groups * (int64_t)p.csplit;
   if (blocks > INT32_MAX || b * s > INT32_MAX) return DSA_ERR_SHAPE;
   if (fused)
@@ -761,8 +760,7 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
     sp.psort = p.psort;
     sp.offset = offset;
     const size_t smem2 = 1024 * 4 + 16 + 16 + (size_t)ps * 8;
-    if (hipFuncSetAttribute((const void*)ix_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)smem2) != hipSuccess)
+    if (dsa_host::ensure_dyn_lds((const void*)ix_select_kernel, (int)smem2) != DSA_OK)
       return DSA_ERR_LAUNCH;
     hipLaunchKernelGGL(ix_select_kernel, dim3((unsigned)(b * s)), dim3(256), smem2, stream, sp);
     if (hipGetLastError() != hipSuccess) return DSA_ERR_LAUNCH;

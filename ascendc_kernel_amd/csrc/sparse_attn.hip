@@ -21,6 +21,9 @@
 // every lane loads and stores 16 contiguous bytes of a row.
 #include "dsa_common.h"
 
+#include <atomic>
+#include <mutex>
+
 using namespace dsa;
 
 namespace {
@@ -308,17 +311,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 }  // namespace
 
 namespace dsa_host {
+// The CU count of each device, queried once. Relaxed atomics: threads that race
+// on the first call of a device store the same value.
 int device_cu_count(int* out) {
-  static int cached[64];
+  static std::atomic<int> cached[kMaxDevices];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DSA_ERR_DEVICE;
-  if (cached[dev] <= 0) {
-    int cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return DSA_ERR_DEVICE;
+  int cu = cached[dev].load(std::memory_order_relaxed);
+  if (cu <= 0) {
     if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0)
       return DSA_ERR_DEVICE;
-    cached[dev] = cu;
+    cached[dev].store(cu, std::memory_order_relaxed);
   }
-  *out = cached[dev];
+  *out = cu;
+  return DSA_OK;
+}
+
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per (kernel, device) and
+// size: the limit only ever grows, and a launch asking for no more than what was
+// set skips the runtime call (it costs microseconds per launch otherwise).
+int ensure_dyn_lds(const void* fn, int bytes) {
+  struct Entry {
+    const void* fn;
+    int dev;
+    int bytes;
+  };
+  static std::mutex mu;
+  static Entry tab[256];
+  static int n = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return DSA_ERR_DEVICE;
+  std::lock_guard<std::mutex> lock(mu);
+  Entry* e = nullptr;
+  for (int i = 0; i < n; ++i)
+    if (tab[i].fn == fn && tab[i].dev == dev) e = &tab[i];
+  if (e != nullptr && e->bytes >= bytes) return DSA_OK;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
+    return DSA_ERR_LAUNCH;
+  if (e != nullptr) e->bytes = bytes;
+  else if (n < 256) tab[n++] = Entry{fn, dev, bytes};
   return DSA_OK;
 }
 }  // namespace dsa_host

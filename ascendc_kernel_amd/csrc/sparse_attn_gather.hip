@@ -19,6 +19,8 @@
 // high part and a bf16 residual so that the PV product keeps ~16 bits of P.
 #include "dsa_common.h"
 
+#include <float.h>
+
 using namespace dsa;
 
 namespace {
@@ -172,7 +174,9 @@ void sa_gather_kernel(GatherParams p) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
   const float sink_l2 = hvalid ? sink_raw * kLog2e : 0.f;
   const float c2 = p.scale_log2;  // > 0 (checked by the host)
-  float m_run = sink_l2;   // running max (log2 units) incl. the sink
+  // Running max (log2 units) incl. the sink, floored at -FLT_MAX so that a -inf
+  // sink with a fully masked first block gives exp2(-inf) = 0, not NaN.
+  float m_run = fmaxf(sink_l2, -FLT_MAX);
   float l_run = 0.f;       // this lane's partial sum of exp2(s - m_run)
 
   // S^T = K . Q^T for the block in LDS buffer kvl: A = K rows (key = lane%32,

@@ -20,6 +20,8 @@
 // The two waves of a SIMD overlap one's softmax with the other's products.
 #include "dsa_common.h"
 
+#include <float.h>
+
 using namespace dsa;
 
 namespace {
@@ -163,7 +165,10 @@ void sa_mla_kernel(MlaParams p) {
   for (int ct = 0; ct < kCT; ++ct) o[ct] = f32x4{};
   const float sink_l2 = sink_raw * kLog2e;
   const float c2 = p.scale_log2;  // > 0 (checked by the host)
-  float m_run = sink_l2;
+  // The running max starts at the sink, floored at -FLT_MAX: with a -inf sink and
+  // a fully masked first block, exp2(s * c2 - m_run) is then exp2(-inf) = 0
+  // instead of exp2(-inf + inf) = NaN.
+  float m_run = fmaxf(sink_l2, -FLT_MAX);
   float l_run = 0.f;
 
   // S^T of the block in buffer kvl: tile kt has keys 16kt + (lane%16) as A rows,
@@ -456,8 +461,8 @@ int mla_launch(const MlaParams& p, int nw, size_t smem, hipStream_t st) {
   switch (nw) {
 #define DSA_MLA_CASE(n)                                                                           \
   case n:                                                                                         \
-    if (hipFuncSetAttribute((const void*)sa_mla_kernel<n, IdxT, kSplit>,                           \
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)   \
+    if (dsa_host::ensure_dyn_lds((const void*)sa_mla_kernel<n, IdxT, kSplit>, (int)smem) !=      \
+        DSA_OK)                                                                                   \
       return DSA_ERR_LAUNCH;                                                                      \
     hipLaunchKernelGGL((sa_mla_kernel<n, IdxT, kSplit>), grid, dim3(64 * n), smem, st, p);        \
     break;
@@ -485,6 +490,9 @@ int sparse_mla_fwd(const void* q, const void* kv, const void* topk_idxs, bool id
   if (h % 16 != 0 || h < 64 || h > 128 || topk > 2048) return DSA_ERR_UNSUPPORTED;
   if (!(softmax_scale > 0.f) || !(softmax_scale < INFINITY)) return DSA_ERR_UNSUPPORTED;
   if (n_kv > (1 << 21) || kv_dim > (1 << 16) || (kv_dim % 8) != 0) return DSA_ERR_UNSUPPORTED;
+  // The kernel addresses a batch's kv rows through one buffer resource whose size
+  // and row offsets are 32-bit byte counts.
+  if (n_kv * kv_dim * 2 > (int64_t)UINT32_MAX) return DSA_ERR_UNSUPPORTED;
   if (b * m > INT32_MAX) return DSA_ERR_SHAPE;
   if (b == 0 || m == 0) return DSA_OK;
   if (!q || !kv || !topk_idxs || !attn_sink || !out) return DSA_ERR_NULL;
@@ -563,9 +571,10 @@ extern "C" int dsa_sparse_mla_fwd_i64(const void* q, const void* kv, const int64
 }
 
 extern "C" int64_t dsa_sparse_mla_workspace_bytes(int64_t b, int64_t m, int64_t h, int64_t topk) {
-  if (b <= 0 || m <= 0 || h <= 0 || topk <= 0 || b * m > INT32_MAX) return 0;
+  if (b < 0 || m < 0 || h <= 0 || topk <= 0 || b * m > INT32_MAX) return DSA_ERR_SHAPE;
+  if (b == 0 || m == 0) return 0;
   int cu = 0;
-  if (dsa_host::device_cu_count(&cu) != DSA_OK) return 0;
+  if (dsa_host::device_cu_count(&cu) != DSA_OK) return DSA_ERR_DEVICE;
   int nsplit, bps;
   mla_split_plan(b * m, topk, cu, &nsplit, &bps);
   return mla_split_bytes(b * m, h, nsplit);

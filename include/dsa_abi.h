@@ -7,8 +7,11 @@
  *
  * Conventions shared by every entry point:
  *   - All pointers are device pointers (HBM) except where noted; the caller
- *     owns every buffer. The library never allocates and keeps no state
- *     between calls, so calls on different streams may run concurrently.
+ *     owns every buffer. The library never allocates device memory. Its only
+ *     state between calls is a
+ *     per-device cache of the CU count and of the LDS limits already set per
+ *     kernel, filled on first use and thread-safe; calls on different streams
+ *     may run concurrently.
  *   - Tensors are dense and row-major (C-contiguous) unless a stride argument
  *     says otherwise. bf16 tensors are passed as raw 16-bit words.
  *   - `stream` is a hipStream_t (NULL = the legacy default stream). Launches
@@ -100,7 +103,10 @@ int dsa_sparse_attn_fwd_i64(const void* q, const void* kv, const int64_t* topk_i
  *   attn_sink  fp32 [h]
  *   out        bf16 [b, m, h, d_v]
  * Requirements: d_qk == 576, d_v == 512, h % 16 == 0 with 64 <= h <= 128,
- * topk <= 2048, n_kv <= 2^21, kv_dim % 8 == 0, softmax_scale > 0; q/kv/out 16-byte aligned.
+ * topk <= 2048, n_kv <= 2^21, kv_dim % 8 == 0, n_kv * kv_dim * 2 <= 2^32 - 1 (a batch's
+ * kv rows are addressed with 32-bit byte offsets), softmax_scale > 0; q/kv/out
+ * 16-byte aligned. A -inf sink is allowed; with every slot masked and a -inf sink the
+ * output is NaN, as in the reference (its denominator is exp(-inf - (-inf))).
  */
 int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* topk_idxs,
                        const float* attn_sink, void* out, int64_t b, int64_t m, int64_t h,
@@ -122,7 +128,9 @@ int dsa_sparse_mla_fwd_i64(const void* q, const void* kv, const int64_t* topk_id
  * than CUs (decode), each token's slot list is split among several workgroups
  * whose fp32 partial results go to the workspace and are merged by a second
  * kernel. Returns 0 when no split applies (then the _ws calls run the one-pass
- * kernel and need no workspace).
+ * kernel and need no workspace, also for b * m == 0), DSA_ERR_SHAPE for invalid
+ * sizes and DSA_ERR_DEVICE when the device cannot be queried (a negative value is
+ * never a size).
  * Same computation as sparse_attn_ref (reference/task1_v0_ref.py:5-24) with
  * v_dim 512; the split changes only the fp32 summation order of the softmax sums.
  */
@@ -195,7 +203,7 @@ int dsa_indexer_score_topk(const void* q, const void* kv_cache, int64_t kv_batch
 
 /*
  * Workspace for dsa_indexer_score_topk_ws, in bytes (0: the configuration needs none;
- * -1: invalid sizes). For h == 64, d == 128 it is b * s * n_cand * 2 (one 16-bit order
+ * DSA_ERR_SHAPE: invalid sizes). For h == 64, d == 128 it is b * s * n_cand * 2 (one 16-bit order
  * key per token and candidate).
  */
 int64_t dsa_indexer_workspace_bytes(int64_t b, int64_t s, int64_t h, int64_t d, int64_t n_cand);

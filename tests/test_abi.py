@@ -152,11 +152,14 @@ def test_int64_index_entry_points_host_checks():
     assert g(*m[:6], 0, *m[7:]) == 0
     assert g(*m[:2], None, *m[3:]) == -1                 # no topk_idxs
     assert g(*m[:4], None, *m[5:]) == -1                 # no out
+    # a batch's kv rows beyond 4 GiB: 32-bit row offsets would wrap
+    assert g(*m[:10], 1024, 1 << 21, *m[12:]) == -3
 
 
 def test_sparse_mla_workspace_entry_points_host_checks():
     """dsa_sparse_mla_fwd_ws / _i64_ws check shapes like dsa_sparse_mla_fwd and reject a
-    negative workspace size; the workspace query is 0 for empty or invalid requests."""
+    negative workspace size; the workspace query is 0 for empty requests and a negative
+    DSA_ERR_* code (never a size) for invalid ones."""
     lib = _native.load()
     m = [16, 16, 16, 16, 16, 1, 1, 128, 576, 512, 576, 100, 64, 576 ** -0.5, 16, 1 << 20, None]
     for f in (lib.dsa_sparse_mla_fwd_ws, lib.dsa_sparse_mla_fwd_i64_ws):
@@ -166,7 +169,8 @@ def test_sparse_mla_workspace_entry_points_host_checks():
         assert f(*m[:6], 0, *m[7:]) == 0
         assert f(*m[:2], None, *m[3:]) == -1
     assert lib.dsa_sparse_mla_workspace_bytes(0, 1, 128, 2048) == 0
-    assert lib.dsa_sparse_mla_workspace_bytes(1, 1, 128, 0) == 0
+    assert lib.dsa_sparse_mla_workspace_bytes(1, 1, 128, 0) == -2
+    assert lib.dsa_sparse_mla_workspace_bytes(-1, 1, 128, 64) == -2
 
 
 def _ixw(lib, **kw):
@@ -197,7 +201,7 @@ def test_workspace_bytes():
     assert lib.dsa_indexer_workspace_bytes(1, 8192, 64, 128, 8192) == 8192 * 8192 * 2
     assert lib.dsa_indexer_workspace_bytes(2, 100, 64, 128, 512) == 2 * 100 * 512 * 2
     assert lib.dsa_indexer_workspace_bytes(8, 2600, 16, 64, 650) == 0   # the 16-head kernel needs none
-    assert lib.dsa_indexer_workspace_bytes(-1, 8, 64, 128, 64) == -1
+    assert lib.dsa_indexer_workspace_bytes(-1, 8, 64, 128, 64) == -2
 
 
 def test_indexer_scores_host_checks():
@@ -210,3 +214,4 @@ def test_indexer_scores_host_checks():
     bad = list(args)
     bad[13] = 0                                                          # no candidates
     assert lib.dsa_indexer_scores(*bad) == -2
+

@@ -205,6 +205,22 @@ def test_gather_shapes_and_masks(gpu, case):
     _compare(out, ref, f"gather{case}")
 
 
+@pytest.mark.parametrize("variant", [_native.DSA_SA_GATHER, _native.DSA_SA_MULTIPLICITY])
+def test_neg_inf_sink_masked_leading_block(gpu, variant):
+    """A -inf sink on half the heads with the first slot blocks of every token masked: no
+    NaN from the running max before the first valid slot. (Every slot masked together
+    with a -inf sink is NaN in the reference as well and is not part of the case.)"""
+    n_kv, topk = (700, 200) if variant == _native.DSA_SA_GATHER else (32, 16)
+    q, kv, idx, sink = _case(1, 24, 64, n_kv, topk, 61, 0.0, 1.0)
+    sink[::2] = float("-inf")
+    idx[..., : topk // 2 + 3] = -1
+    _say("-inf sink", variant)
+    out = _native.sparse_attn_fwd(q, kv, idx, sink, 128 ** -0.5, variant)
+    ref = osa.sparse_attn_ref(q, kv, sink, idx, 128 ** -0.5)
+    assert torch.isfinite(ref.float()).all()
+    _compare(out, ref, f"neg-inf-sink-{variant}")
+
+
 def test_gather_equals_multiplicity(gpu):
     """Both variants on the same small-n_kv inputs (duplicates included)."""
     q, kv, idx, sink = _case(2, 64, 64, 32, 16, 27, 0.2, 0.8)

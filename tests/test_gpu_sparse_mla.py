@@ -101,7 +101,7 @@ SPLIT_CASES = [
     (1, 1, 128, 8192, 2048, 31, 0.0, 0.0),    # decode at the configs[4] size
     (1, 4, 128, 8192, 2048, 32, 0.1, 1.0),
     (2, 16, 64, 3000, 300, 33, 0.3, -1.0),    # topk not a multiple of 32, 4 waves
-    (1, 3, 96, 700, 2000, 34, 0.0, 2.0),      # slots beyond n_kv masked in the kernel
+    (1, 3, 96, 700, 2000, 34, 0.0, 2.0),      # slots beyond n_kv (and beyond int32) masked
 ]
 
 
@@ -111,19 +111,45 @@ def test_mla_split_decode(gpu, case):
     kernel; a split whose whole slot range is masked contributes nothing."""
     b, m, h, n_kv, topk, seed, masked, sink_scale = case
     q, kv, idx, sink = _case(b, m, h, n_kv, topk, seed, masked, sink_scale)
-    if case[4] == 2000:
-        idx[..., 600:] = -1  # the later splits see only masked slots
+    idx64 = idx.long()
+    if topk == 2000:
+        idx[..., 600:] = -1              # the later splits see only masked slots
+        idx[..., 100:200:7] = n_kv + 5   # at or beyond n_kv: masked in the kernel
+        idx[..., 250:260] = n_kv
+        idx64 = idx.long()
+        idx64[..., 201:300:5] = 2 ** 33 + 1   # beyond int32 (int64 entry point only)
+        idx64[..., 301:320:3] = -(2 ** 40)
+        idx[..., 201:300:5] = -1
+        idx[..., 301:320:3] = -1
     lib = _native.load()
     assert lib.dsa_sparse_mla_workspace_bytes(b, m, h, topk) > 0, "expected a split plan"
     _say("mla split case", case)
     out = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV)
     one = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV, split=False)
-    i64 = _native.sparse_mla_fwd(q, kv, idx.long(), sink, SCALE, DV)
+    i64 = _native.sparse_mla_fwd(q, kv, idx64, sink, SCALE, DV)
     assert torch.equal(out.view(torch.int16), i64.view(torch.int16))
-    ref = osa.sparse_attn_ref(q, kv, sink, idx, SCALE, v_dim=DV)
+    ref = osa.sparse_attn_ref(q, kv, sink, torch.where(idx >= n_kv, -1, idx), SCALE, v_dim=DV)
     _compare(out, ref, f"split{case}")
     _compare(one, ref, f"one-pass{case}")
     _compare(out, one, f"split-vs-one-pass{case}")
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_mla_neg_inf_sink_masked_leading_block(gpu, split):
+    """A -inf sink (no sink mass) with the first slot blocks fully masked: the running
+    max must not produce exp2(-inf + inf) = NaN before the first valid slot. Half the
+    heads get -inf, the rest a finite sink; a token with every slot masked and a -inf
+    sink is NaN in the reference too and is left out."""
+    b, m, h, n_kv, topk = 1, 3, 128, 4000, 2048
+    q, kv, idx, sink = _case(b, m, h, n_kv, topk, 41, 0.0, 1.0)
+    sink[::2] = float("-inf")
+    idx[..., :96] = -1                   # blocks 0..2 of every token fully masked
+    idx[0, 1, :1500] = -1                # token 1: most of its splits see only masked slots
+    _say("mla -inf sink", split)
+    out = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV, split=split)
+    ref = osa.sparse_attn_ref(q, kv, sink, idx, SCALE, v_dim=DV)
+    assert torch.isfinite(ref.float()).all()
+    _compare(out, ref, f"mla-neg-inf-sink-split{split}")
 
 
 def test_mla_drop_in_module(gpu):
