@@ -37,6 +37,7 @@ EXPORTS = (
     "dsa_indexer_score_topk",
     "dsa_indexer_workspace_bytes",
     "dsa_indexer_score_topk_ws",
+    "dsa_indexer_score_topk_noalloc",
     "dsa_indexer_scores",
 )
 
@@ -110,6 +111,11 @@ def load() -> ctypes.CDLL:
         _c_vp, _c_vp, _c_i64, _c_vp, ctypes.c_float, _c_vp, ctypes.c_int32, _c_vp,
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
         ctypes.c_int32, _c_i64, _c_vp, _c_i64, _c_vp]
+    lib.dsa_indexer_score_topk_noalloc.restype = ctypes.c_int
+    lib.dsa_indexer_score_topk_noalloc.argtypes = [
+        _c_vp, _c_vp, _c_i64, _c_vp, ctypes.c_float, _c_vp, ctypes.c_int32, _c_vp,
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        ctypes.c_int32, _c_i64, _c_vp]
     lib.dsa_indexer_scores.restype = ctypes.c_int
     lib.dsa_indexer_scores.argtypes = [
         _c_vp, _c_vp, _c_i64, _c_vp, ctypes.c_float, _c_vp, ctypes.c_int32, _c_vp,

@@ -27,6 +27,9 @@
 // first, so the longest causal rows start first.
 #include "dsa_common.h"
 
+#include <atomic>
+#include <mutex>
+
 using namespace dsa;
 
 namespace {
@@ -599,6 +602,61 @@ extern "C" int dsa_indexer_score_topk_ws(const void* q, const void* kv_cache, in
   return launch_ix(q, kv_cache, kv_batch_stride, wl, w_scale, freqs_cis, rope_mode, out, nullptr,
                    b, s, h, d, rd, n_cand, k_out, ratio, causal, offset, workspace, workspace_bytes,
                    stream);
+}
+
+namespace {
+
+// Scratch of dsa_indexer_score_topk_noalloc: the 16-bit order keys of the 64-head
+// path, one per (token, candidate), written by the score kernel and read by the
+// select kernel (every key read was written by the same call). Each device that
+// runs the library holds one copy of this array from module load until the
+// process ends; its device address comes from hipGetSymbolAddress (the array's
+// name in host code is not a device address).
+constexpr int64_t kScratchBytes = DSA_INDEXER_NOALLOC_MAX_BYTES;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Device address of `scratch` on the current device, looked up on the first call
+// from each device and kept.
+int scratch_address(void** out) {
+  static std::atomic<void*> addr[dsa_host::kMaxDevices];
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= dsa_host::kMaxDevices)
+    return DSA_ERR_DEVICE;
+  void* ptr = addr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(mu);
+    ptr = addr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+        return DSA_ERR_DEVICE;
+      addr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return DSA_OK;
+}
+
+}  // namespace
+
+extern "C" int dsa_indexer_score_topk_noalloc(const void* q, const void* kv_cache,
+                                              int64_t kv_batch_stride, const void* wl,
+                                              float w_scale, const void* freqs_cis,
+                                              int32_t rope_mode, int64_t* out, int64_t b,
+                                              int64_t s, int64_t h, int64_t d, int64_t rd,
+                                              int64_t n_cand, int64_t k_out, int64_t ratio,
+                                              int32_t causal, int64_t offset, void* stream) {
+  if (out == nullptr && b > 0 && s > 0) return DSA_ERR_NULL;
+  const int64_t need = dsa_indexer_workspace_bytes(b, s, h, d, n_cand);
+  if (need < 0) return DSA_ERR_SHAPE;
+  if (need > kScratchBytes) return DSA_ERR_SCRATCH;
+  void* ws = nullptr;
+  if (need > 0 && b > 0 && s > 0) {
+    const int rc = scratch_address(&ws);
+    if (rc != DSA_OK) return rc;
+  }
+  return launch_ix(q, kv_cache, kv_batch_stride, wl, w_scale, freqs_cis, rope_mode, out, nullptr,
+                   b, s, h, d, rd, n_cand, k_out, ratio, causal, offset, ws, need, stream);
 }
 
 extern "C" int dsa_indexer_scores(const void* q, const void* kv_cache, int64_t kv_batch_stride,

@@ -365,6 +365,7 @@ extern "C" const char* dsa_strerror(int code) {
     case DSA_ERR_LAUNCH: return "kernel launch failed";
     case DSA_ERR_DEVICE: return "device query failed";
     case DSA_ERR_ALIGN: return "pointer not 16-byte aligned";
+    case DSA_ERR_SCRATCH: return "request exceeds the library's static scratch buffer";
     default: return "unknown error";
   }
 }

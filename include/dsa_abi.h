@@ -7,8 +7,9 @@
  *
  * Conventions shared by every entry point:
  *   - All pointers are device pointers (HBM) except where noted; the caller
- *     owns every buffer. The library never allocates device memory. Its only
- *     state between calls is a
+ *     owns every buffer. The library never allocates device memory (the one
+ *     exception is the static scratch array of dsa_indexer_score_topk_noalloc,
+ *     created when the module loads). Its only state between calls is a
  *     per-device cache of the CU count and of the LDS limits already set per
  *     kernel, filled on first use and thread-safe; calls on different streams
  *     may run concurrently.
@@ -38,6 +39,7 @@ extern "C" {
 #define DSA_ERR_LAUNCH (-4)      /* the HIP runtime rejected a launch */
 #define DSA_ERR_DEVICE (-5)      /* no usable gfx950 device / attribute query failed */
 #define DSA_ERR_ALIGN (-6)       /* a pointer is not 16-byte aligned */
+#define DSA_ERR_SCRATCH (-7)     /* request larger than the library's static scratch buffer */
 
 /* Task1 kernel selection (the `variant` argument of dsa_sparse_attn_fwd). */
 #define DSA_SA_AUTO 0         /* multiplicity kernel when n_kv <= 32, else gather */
@@ -223,6 +225,29 @@ int dsa_indexer_score_topk_ws(const void* q, const void* kv_cache, int64_t kv_ba
                               int64_t h, int64_t d, int64_t rd, int64_t n_cand, int64_t k_out,
                               int64_t ratio, int32_t causal, int64_t offset, void* workspace,
                               int64_t workspace_bytes, void* stream);
+
+/*
+ * dsa_indexer_score_topk_ws without a caller workspace and without any allocation:
+ * the workspace is a static device array of DSA_INDEXER_NOALLOC_MAX_BYTES inside the
+ * library (one per device, held from module load until the process ends). Same
+ * arguments and results as dsa_indexer_score_topk. Returns DSA_ERR_SCRATCH when
+ * dsa_indexer_workspace_bytes(b, s, h, d, n_cand) exceeds that size (64 heads x 128:
+ * b * s * n_cand <= 8,388,608, e.g. 1024 tokens at 8192 candidates); configurations
+ * that need no workspace (16 heads x 64) run as dsa_indexer_score_topk. Calls on one
+ * device share the array, so calls that overlap on one device (different streams)
+ * race; calls ordered on one stream do not. No hipMalloc/hipFree or other allocating
+ * call is made, so it can be used where the caller cannot allocate (inside HIP graph
+ * capture, allocation-free serving loops).
+ * No counterpart in the reference: an addition for callers that cannot allocate;
+ * it computes what dsa_indexer_score_topk does (reference/task2_v0_ref.py:131-143).
+ */
+#define DSA_INDEXER_NOALLOC_MAX_BYTES (INT64_C(16) << 20)
+int dsa_indexer_score_topk_noalloc(const void* q, const void* kv_cache, int64_t kv_batch_stride,
+                                   const void* wl, float w_scale, const void* freqs_cis,
+                                   int32_t rope_mode, int64_t* out, int64_t b, int64_t s,
+                                   int64_t h, int64_t d, int64_t rd, int64_t n_cand,
+                                   int64_t k_out, int64_t ratio, int32_t causal, int64_t offset,
+                                   void* stream);
 
 /*
  * Task2 score stage alone: writes the bf16 index_score [b, s, n_cand] that the reference

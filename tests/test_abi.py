@@ -31,7 +31,7 @@ def test_exports_every_declared_symbol():
 def test_strerror():
     lib = _native.load()
     assert lib.dsa_strerror(0) == b"ok"
-    for code in (-1, -2, -3, -4, -5, -6):
+    for code in (-1, -2, -3, -4, -5, -6, -7):
         assert lib.dsa_strerror(code) not in (b"ok", b"unknown error")
     assert lib.dsa_strerror(-99) == b"unknown error"
 
@@ -215,3 +215,23 @@ def test_indexer_scores_host_checks():
     bad[13] = 0                                                          # no candidates
     assert lib.dsa_indexer_scores(*bad) == -2
 
+
+def test_indexer_noalloc_host_checks():
+    """dsa_indexer_score_topk_noalloc: requests beyond the static scratch array are refused
+    with DSA_ERR_SCRATCH before anything runs; shape and pointer checks as the _ws form."""
+    lib = _native.load()
+
+    def f(**kw):
+        a = dict(q=16, kv=16, kvbs=8192 * 128, wl=16, scale=0.011, fr=16, mode=1, out=16, b=1, s=8192,
+                 h=64, d=128, rd=64, T=8192, K=2048, ratio=1, causal=1, offset=0)
+        a.update(kw)
+        return lib.dsa_indexer_score_topk_noalloc(
+            a["q"], a["kv"], a["kvbs"], a["wl"], a["scale"], a["fr"], a["mode"], a["out"], a["b"],
+            a["s"], a["h"], a["d"], a["rd"], a["T"], a["K"], a["ratio"], a["causal"], a["offset"], None)
+
+    assert f() == -7                      # 8192 x 8192 keys: 128 MiB > 16 MiB
+    assert f(s=1025, T=8192) == -7        # one token row beyond 8,388,608 keys
+    assert lib.dsa_strerror(-7) == b"request exceeds the library's static scratch buffer"
+    assert f(b=-1) == -2
+    assert f(out=None) == -1
+    assert f(s=0) == 0
