@@ -19,6 +19,14 @@ Fixtures
                     output only (inputs are regenerated from the seed; their sha256 is stored)
   task2_small.npz   task2_v0_ref.Model built under torch.manual_seed(42) with a reduced
                     ModelArgs; weights, inputs and outputs for start_pos 0 and 64
+  task2_freqs.npz   the RoPE table of task2_v0_ref.get_init_inputs (:162-172) under
+                    torch.manual_seed(42): sha256 of freqs_cis and kv_cache, the first and
+                    last rows of freqs_cis; the same for the configs[4] table (rope_head_dim
+                    64, max_seq_len 8192, through the reference's own get_init_inputs with
+                    its _make_args returning those arguments)
+
+    python tests/golden/make_golden.py [/root/reference] [task1|task2|freqs ...]
+writes the named fixtures (all of them by default).
 """
 from __future__ import annotations
 
@@ -122,11 +130,39 @@ def task2(ref_dir: str) -> None:
         torch.Tensor.cuda = saved
 
 
+def freqs(ref_dir: str) -> None:
+    saved = torch.Tensor.cuda
+    torch.Tensor.cuda = lambda self, *a, **k: self
+    try:
+        t2 = _load(os.path.join(ref_dir, "reference", "task2_v0_ref.py"), "task2_v0_ref")
+        out = {}
+        torch.manual_seed(42)
+        _, fc, kv, ratio = t2.get_init_inputs()
+        out.update(c3_sha=np.bytes_(_sha(torch.view_as_real(fc))), c3_kv_sha=np.bytes_(_sha(kv)),
+                   c3_shape=np.array(fc.shape, np.int64), c3_ratio=np.int64(ratio),
+                   c3_head=torch.view_as_real(fc[:4]).numpy(), c3_tail=torch.view_as_real(fc[-4:]).numpy())
+        orig = t2._make_args
+        t2._make_args = lambda: t2.ModelArgs(max_batch_size=1, max_seq_len=8192, dim=7168,
+                                             index_n_heads=64, index_head_dim=128, index_topk=2048,
+                                             q_lora_rank=1536, rope_head_dim=64)
+        try:
+            torch.manual_seed(42)
+            _, fc, kv, _ = t2.get_init_inputs()
+        finally:
+            t2._make_args = orig
+        out.update(c5_sha=np.bytes_(_sha(torch.view_as_real(fc))), c5_shape=np.array(fc.shape, np.int64),
+                   c5_head=torch.view_as_real(fc[:4]).numpy(), c5_tail=torch.view_as_real(fc[-4:]).numpy())
+        np.savez_compressed(os.path.join(HERE, "task2_freqs.npz"), **out)
+    finally:
+        torch.Tensor.cuda = saved
+
+
 if __name__ == "__main__":
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    which = sys.argv[2:] or ["task1", "task2", "freqs"]
     torch.set_num_threads(1)
-    task1(ref)
-    task2(ref)
+    for name in which:
+        {"task1": task1, "task2": task2, "freqs": freqs}[name](ref)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -204,9 +204,14 @@ def test_separate_rope_equals_fused(gpu):
 
 
 def test_reference_fixture_cpu_rounding(gpu):
-    """Reference fixture (computed on the CPU): feed the kernel the CPU projections and the CPU
-    RoPE rounding. Remaining differences can only come from the CPU's topk tie order and GEMM
-    accumulation order; report the agreement and require it to be high."""
+    """Reference fixture (computed by the reference on the CPU): the kernel gets the CPU
+    projections and the CPU RoPE rounding. Its rows may still differ from the fixture for
+    two reasons only, and every differing row must be one of them:
+      ties   the picks differ only among candidates whose reference score equals the row's
+             k-th score (the CPU's topk order of equal values is not stable), or
+      device the reference's CPU score and the kernel's score (torch-ROCm's GEMM and
+             head-sum order) differ on a candidate the two picks disagree on.
+    The kernel's indices are also exactly torch-ROCm's top-k of its own scores."""
     f = np.load(os.path.join(GOLDEN, "task2_small.npz"))
     wq, ww = bf16_from_bits(f["wq"]), bf16_from_bits(f["ww"])
     x, qr = bf16_from_bits(f["x"]), bf16_from_bits(f["qr"])
@@ -214,14 +219,37 @@ def test_reference_fixture_cpu_rounding(gpu):
     wl = torch.nn.functional.linear(x, ww)
     fr = torch.view_as_complex(torch.from_numpy(f["freqs"]).contiguous())
     kv = bf16_from_bits(f["kv"])
+    scale, k, n_cand = 64 ** -0.5 * 16 ** -0.5, 32, 64
     _say("case reference fixture")
-    got = _native.indexer_score_topk(q.to(gpu), kv.to(gpu), wl.to(gpu), 64 ** -0.5 * 16 ** -0.5,
-                                     fr.to(gpu)[:256], 32, 64, 32, 4, True, 0, _native.DSA_ROPE_CPU).cpu()
-    want = torch.from_numpy(f["out0"])
-    same_rows = (got == want).all(dim=-1).float().mean().item()
-    same_sets = np.mean([set(a.tolist()) == set(b.tolist()) for a, b in zip(got.view(-1, 32), want.view(-1, 32))])
-    _say(f"fixture agreement: rows {same_rows:.4f}, sets {same_sets:.4f}")
-    assert same_sets > 0.97
+    got = _native.indexer_score_topk(q.to(gpu), kv.to(gpu), wl.to(gpu), scale, fr.to(gpu)[:256], 32,
+                                     n_cand, k, 4, True, 0, _native.DSA_ROPE_CPU).cpu().numpy().reshape(-1, k)
+    s_dev = bits_of(_native.indexer_scores(q.to(gpu), kv.to(gpu), wl.to(gpu), scale, fr.to(gpu)[:256], 32,
+                                           n_cand, 4, True, _native.DSA_ROPE_CPU)).reshape(-1, n_cand)
+    # the reference's own scores: the oracle on the CPU (equal to the reference there)
+    s_ref = bits_of(oix.index_scores(wq, ww, kv, fr, x, qr, 0, 16, 64, 32, 4)).reshape(-1, n_cand)
+    want = f["out0"].reshape(-1, k)
+    t = np.tile(np.arange(256), 2)
+    n_r = np.minimum((t + 1) // 4, n_cand)
+    assert np.array_equal(got, rules.fill(rules.topk_torch(s_dev, k), n_r, True, 0))
+    key_ref = rules.order_key(s_ref).astype(np.int64)
+    n_tie = n_dev = 0
+    for r in np.nonzero((got != want).any(axis=1))[0]:
+        g_ok, w_ok = got[r][got[r] >= 0], want[r][want[r] >= 0]
+        assert len(g_ok) == len(w_ok), r
+        kg, kw = np.sort(key_ref[r][g_ok])[::-1], np.sort(key_ref[r][w_ok])[::-1]
+        if np.array_equal(kg, kw) and np.all(np.diff(key_ref[r][g_ok]) <= 0):
+            n_tie += 1
+            continue
+        # candidates in contention: at or above the k-th score on either device
+        key_dev = rules.order_key(s_dev[r]).astype(np.int64)
+        kth_ref = np.sort(key_ref[r])[::-1][k - 1]
+        kth_dev = np.sort(key_dev)[::-1][k - 1]
+        top = (key_ref[r] >= kth_ref) | (key_dev >= kth_dev)
+        assert ((s_dev[r] != s_ref[r]) & top).any(), f"row {r}: picks differ beyond ties with equal scores"
+        n_dev += 1
+    same_rows = float((got == want).all(axis=1).mean())
+    _say(f"fixture: rows equal {same_rows:.4f}; differing rows: {n_tie} ties at the k-th score, "
+         f"{n_dev} with CPU/GPU score differences ({int((s_dev != s_ref).sum())} of {s_ref.size} scores differ)")
 
 
 @pytest.mark.parametrize("seqlen,start_pos", [(2600, 0), (301, 0), (64, 64), (120, 0)])

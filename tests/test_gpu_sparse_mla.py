@@ -205,3 +205,44 @@ def test_dsa_layer_indexer_then_mla(gpu):
     out = attn(qm, kvm, topk_idxs)
     ref = osa.sparse_attn_ref(qm, kvm, attn.attn_sink, topk_idxs, attn.softmax_scale, v_dim=DV)
     _compare(out, ref, "dsa-layer")
+
+
+def test_dsa_layer_c5_full_size_chained(gpu):
+    """configs[4] prefill chained as in the reference (task2_v0_ref.py:138-143 output is
+    task1_v0_ref.py:8-12's topk_idxs): the indexer Model.forward at 8192 tokens with
+    W ~ N(0, 0.02) gives int64 top-2048 picks equal to the oracle's on the same GPU; they
+    go unchanged into Model(128, 576, v_dim=512), whose output is checked on every 32nd
+    token (and the last) against the oracle's attention over the same picks."""
+    torch.manual_seed(42)
+    init = t2.get_c5_init_inputs(device=gpu)
+    ix = t2.Model(*init).to(gpu)
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        for p in (ix.wq_b.weight, ix.weights_proj.weight):
+            p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(torch.bfloat16))
+    r = oix.IndexerRef(*init).to(gpu)
+    r.wq_b.weight.data.copy_(ix.wq_b.weight.data)
+    r.weights_proj.weight.data.copy_(ix.weights_proj.weight.data)
+    x, qr, sp, off = t2.get_c5_inputs(device=gpu)
+    _say("case c5 chained: indexer")
+    with torch.no_grad():
+        picks = ix(x, qr, sp, off)
+        torch.cuda.synchronize()
+        _say("case c5 chained: indexer oracle")
+        want = r(x, qr, sp, off)
+        torch.cuda.synchronize()
+    assert picks.dtype == torch.int64 and tuple(picks.shape) == (1, 8192, 2048)
+    assert torch.equal(picks, want)
+    del x, qr, want, r
+    torch.cuda.empty_cache()
+    qm, kvm, _ = t1.get_mla_inputs(device=gpu)
+    attn = t1.Model(128, DQK, v_dim=DV).to(gpu)
+    _say("case c5 chained: sparse MLA over the indexer's picks")
+    out = attn(qm, kvm, picks)
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, 8192, 32), torch.tensor([8191])]).to(gpu)
+    _say("case c5 chained: oracle attention")
+    ref = torch.cat([osa.sparse_attn_ref(qm[:, rows[i:i + 32]], kvm, attn.attn_sink, picks[:, rows[i:i + 32]],
+                                         attn.softmax_scale, v_dim=DV) for i in range(0, len(rows), 32)], dim=1)
+    exact = _compare(out[:, rows], ref, "c5-chained")
+    assert exact > 0.97

@@ -183,3 +183,29 @@ def test_head_sum_split2_rule():
     even, odd = rules.head_sum(w[:, 0::2], "rocm"), rules.head_sum(w[:, 1::2], "rocm")
     assert np.array_equal(s2, (even + odd).astype(np.float32))
     assert not np.array_equal(s2, rules.head_sum(w, "rocm"))
+
+
+def test_freqs_cis_matches_reference_table():
+    """precompute_freqs_cis (oracle and product) against the RoPE table the reference's own
+    get_init_inputs builds (task2_v0_ref.py:162-172; fixture written by importing it): the
+    configs[2] table and the configs[4] one (rope_head_dim 64, 8192 positions), bit for bit,
+    and get_init_inputs' kv_cache draw under seed 42."""
+    import hashlib
+    from ascendc_kernel_amd import task2_indexer as t2
+
+    f = np.load(os.path.join(GOLDEN, "task2_freqs.npz"))
+
+    def sha(t):
+        return hashlib.sha256(t.contiguous().view(torch.uint8).numpy().tobytes()).hexdigest().encode()
+
+    for key, rd, n in (("c3", 32, 2600), ("c5", 64, 8192)):
+        for fc in (oix.precompute_freqs_cis(rd, n), t2.precompute_freqs_cis(rd, n, device="cpu")):
+            assert tuple(fc.shape) == tuple(f[f"{key}_shape"])
+            re = torch.view_as_real(fc)
+            assert np.array_equal(re[:4].numpy(), f[f"{key}_head"]) and np.array_equal(re[-4:].numpy(), f[f"{key}_tail"])
+            assert sha(re) == bytes(f[f"{key}_sha"]), key
+    torch.manual_seed(42)
+    _, fc, kv, ratio = t2.get_init_inputs(device="cpu")
+    assert ratio == int(f["c3_ratio"])
+    assert sha(torch.view_as_real(fc)) == bytes(f["c3_sha"])
+    assert sha(kv) == bytes(f["c3_kv_sha"])
