@@ -8,22 +8,27 @@
 //   w     (:132)  bf16(fp32(wl) * fp32(scale))
 //   S     (:133)  bf16(q . k), fp32 accumulation over channels 0..127 in order
 //   score (:134)  bf16(sum_h bf16(relu(S_h) * w_h)), fp32 sum in the order of
-//                 torch's reduction kernel for a 64-long middle dimension when the
-//                 candidate count is a multiple of 4: two threads take the even and
-//                 the odd heads; each keeps four accumulators over its heads
-//                 (accumulator i of thread y gets heads y + 2i + 8m, m = 0..7, in
-//                 order) combined as ((a0 + a1) + a2) + a3; then even + odd.
+//                 torch's reduction kernel for a 64-long middle dimension: Y threads
+//                 split the heads (thread y takes heads y, y + Y, ...), each keeps
+//                 four accumulators over its heads (accumulator i of thread y gets
+//                 heads y + Y i + 4 Y m in order) combined as ((a0 + a1) + a2) + a3,
+//                 and the thread totals meet in a halving tree (Y = 2: t0 + t1;
+//                 Y = 4: (t0 + t2) + (t1 + t3)). Y follows from the candidate count
+//                 T and the output size N = b s T (torch_head_split below; measured
+//                 on the MI355X for T up to 8192 and N up to 132 K).
 //   mask / top-k / fill (:135-143) as in the 16-head kernel; ties by index.
 //
-// Workgroup = 4 consecutive tokens x 2 waves (even heads, odd heads). The
-// candidates go in tiles of 32 keys (8 KB), copied into a 4-buffer LDS ring by
-// buffer_load ... lds and shared by the 8 waves. A wave computes
+// Workgroup = 4 consecutive tokens x 2 waves (32 heads each). The candidates go
+// in tiles of 32 keys (8 KB), copied into a 4-buffer LDS ring by buffer_load ... lds
+// and shared by the 8 waves. A wave computes
 //   S[32 heads x 32 candidates] = Q[32 x 128] . K^T   (8 x mfma 32x32x16)
-// with its 32 head rows permuted so that every lane holds, for one candidate,
-// 2 of its thread's 4 accumulators complete (8 heads each, in order): the
+// with its 32 head rows permuted (head_of) so that the 16 heads a lane holds for
+// one candidate form whole accumulator chains of the order above: Y = 2, wave y =
+// thread y, lane half hf = its accumulators 2hf, 2hf+1; Y = 4, lane half hf of wave
+// y = thread y + 2hf; Y = 1, lane half hf of wave y = accumulator 2(1 - y) + hf. The
 // relu/w/bf16 chain and the sums are lane-local (relu with v_pk_max_i16 on the
-// packed bf16 scores, exact fp32 products, IEEE fp32 adds), one v_permlane32_swap joins
-// the lane halves, and the even/odd totals meet in LDS. Scores become 16-bit
+// packed bf16 scores, exact fp32 products, IEEE fp32 adds), one v_permlane32_swap
+// joins the lane halves, and the two waves' totals meet in LDS. Scores become 16-bit
 // order keys in LDS; per token a two-pass 8-bit radix select finds the k-th key,
 // the picks are compacted ([> k-th] then [== k-th] in index order) and put in
 // (key descending, index ascending) order by a stable two-pass LSD radix sort
@@ -56,6 +61,7 @@ struct WideParams {
   uint16_t* gkeys;      // if set: per-candidate results go to this [B*S, T] buffer instead of
                         // LDS and the kernel ends after the scores (no top-k)
   int32_t graw;         // 1: gkeys gets the bf16 scores (masked -inf); 0: 16-bit order keys
+  int64_t gstride;      // gkeys row length: T for the scores, T rounded up to 4 for keys
   int32_t B, S, rd, T, K, ratio, causal;
   int64_t offset;
   int32_t groups;       // ceil(S / kTok)
@@ -67,13 +73,23 @@ struct WideParams {
 
 __device__ __forceinline__ int swz(int r, int c) { return r * 16 + (c ^ (r & 15)); }
 
-// Head of MFMA row R in the wave for head parity y: lane half hf = (R/4)%2 and
-// register r = 4(R/8) + R%4 hold head y + 4hf + 2(r%2) + 8(r/2), so a lane has
-// accumulators 2hf and 2hf+1 (heads y + 2i + 8m) for m = 0..7 in registers
-// 2m and 2m+1.
+// Head held in accumulator register r (0..15) of lane half hf of wave y, for the
+// head split KY (register pair m = r/2 is one packed bf16 pair in the score loop):
+//  KY = 2: thread y, accumulator i = 2hf + r%2, term m       -> y + 2i + 8m
+//  KY = 4: thread y + 2hf, accumulator i = 2(m%2) + r%2, term m/2
+//                                                           -> y + 2hf + 4i + 16(m/2)
+//  KY = 1: accumulator i = 2(1 - y) + hf, term r            -> i + 4r
+template <int KY>
+__device__ __forceinline__ int head_of(int y, int hf, int r) {
+  const int m = r >> 1;
+  if constexpr (KY == 2) return y + 2 * (2 * hf + (r & 1)) + 8 * m;
+  else if constexpr (KY == 4) return y + 2 * hf + 4 * (2 * (m & 1) + (r & 1)) + 16 * (m >> 1);
+  else return 2 * (1 - y) + hf + 4 * r;
+}
+// MFMA row R of the 32x32 accumulator sits in lane half (R/4)%2, register 4(R/8) + R%4.
+template <int KY>
 __device__ __forceinline__ int head_of_row(int R, int y) {
-  const int r = 4 * (R >> 3) + (R & 3);
-  return y + 4 * ((R >> 2) & 1) + 2 * (r & 1) + 8 * (r >> 1);
+  return head_of<KY>(y, (R >> 2) & 1, 4 * (R >> 3) + (R & 3));
 }
 
 __device__ __forceinline__ int n_valid_w(const WideParams& p, int t) {
@@ -335,8 +351,9 @@ __device__ void select_topk_row(const uint16_t* keys, int nv, int K, uint32_t* h
 // the top-k (select_topk_row) at the end. Otherwise the per-candidate results go
 // to p.gkeys and the kernel ends after the scores; that instantiation carries no
 // select code, which keeps its register count low enough for two workgroups per CU.
-template <bool kFused>
+template <bool kFused, int KY>
 __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
+  static_assert(KY == 1 || KY == 2 || KY == 4, "torch splits 64 heads over 1, 2 or 4 threads");
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* keys = reinterpret_cast<uint16_t*>(smem);                                   // [kTok][tpad]
   u32x4* ring = reinterpret_cast<u32x4*>(smem + (size_t)kTok * p.tpad * 2);           // [kRingW][512]
@@ -373,7 +390,7 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
   uint16_t* mykeys = keys + tl * p.tpad;
 
   // Q fragments (A operand): row col -> head hq; channels 16ks + 8hf .. +7, RoPE'd on the fly.
-  const int hq = head_of_row(col, y);
+  const int hq = head_of_row<KY>(col, y);
   bf16x8 qa[8];
   {
     const uint16_t* qrow = p.q + (row_bt * kWH + hq) * kWD + 8 * hf;
@@ -400,16 +417,15 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
       qa[ks] = __builtin_bit_cast(bf16x8, v);
     }
   }
-  // Head weights of the lane's 16 heads (bf16 bits): wlo[m] = w(h0) in the low half,
-  // whi[m] = w(h0 + 2) in the high half, h0 = y + 4hf + 8m.
+  // Head weights of the lane's 16 heads (bf16 bits): wlo[m] = w of register 2m's head
+  // in the low half, whi[m] = w of register 2m+1's head in the high half.
   uint32_t wlo[8], whi[8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-    const int h0 = y + 4 * hf + 8 * m;
     uint32_t w0 = 0, w1 = 0;
     if (tok_ok) {
-      w0 = f2bf(bf2f(p.wl[row_bt * kWH + h0]) * p.wscale);
-      w1 = f2bf(bf2f(p.wl[row_bt * kWH + h0 + 2]) * p.wscale);
+      w0 = f2bf(bf2f(p.wl[row_bt * kWH + head_of<KY>(y, hf, 2 * m)]) * p.wscale);
+      w1 = f2bf(bf2f(p.wl[row_bt * kWH + head_of<KY>(y, hf, 2 * m + 1)]) * p.wscale);
     }
     wlo[m] = w0;
     whi[m] = w1 << 16;
@@ -435,12 +451,16 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
 #pragma unroll
   for (int m = 0; m < 8; ++m) asm volatile("" ::"v"(wlo[m]), "v"(whi[m]));
 
-  uint16_t* gdst = (p.gkeys != nullptr && tok_ok) ? p.gkeys + row_bt * p.T : nullptr;
-  float t0val = 0.f;  // even-head total of the previous tile (y == 0 waves, upper lanes)
-  // Keys of tile n-1: even + odd totals -> bf16 -> order key (or raw bits when dumping).
+  uint16_t* gdst = (p.gkeys != nullptr && tok_ok) ? p.gkeys + row_bt * p.gstride : nullptr;
+  // Wave 0's part of the previous tile (upper lanes): KY = 2, 4 its total (t0, or
+  // t0 + t2); KY = 1 accumulators a2 (t0val) and a3 (t0val2).
+  float t0val = 0.f, t0val2 = 0.f;
+  // Keys of tile n-1: wave 0's part + wave 1's (from LDS) -> bf16 -> order key (or
+  // raw bits when dumping).
   auto finalize = [&](int n) {
     if (y == 0 && hf == 1) {
-      const float tot = t0val + xbuf[((n & 1) * kTok + tl) * kTileC + col];
+      const float x1 = xbuf[((n & 1) * kTok + tl) * kTileC + col];
+      const float tot = KY == 1 ? (x1 + t0val) + t0val2 : t0val + x1;
       uint32_t sc = f2bf(tot);
       if (p.causal) sc = f2bf(bf2f(sc) + 0.0f);  // the reference adds the 0 / -inf mask
       const int c = kTileC * (nbase + n) + col;
@@ -480,7 +500,9 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
     // (after the last tile this reads a stale slot; the result is not used)
     const u32x4* kt = ring + ((j + 1) % kRingW) * 512;
     s_nx = f32x16{};
-    float acc_a = 0.f, acc_b = 0.f;
+    // acc[i]: the lane's accumulators in the order of head_of (KY = 2: 0, 1; KY = 4:
+    // 0..3; KY = 1: the one chain in acc[0]).
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       s_nx = mfma32x32x16(qa[m], __builtin_bit_cast(bf16x8, kt[swz(col, 2 * m + hf)]), s_nx);
@@ -490,13 +512,36 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
       // with an IEEE fp32 add (v_dot2c's accumulation does not always round like one).
       const uint32_t pv = __builtin_bit_cast(uint32_t, pk);
       const uint32_t pp = pack_bf2(bf_lo(pv) * bf_lo(wlo[m]), bf_hi(pv) * bf_hi(whi[m]));
-      acc_a = acc_a + bf_lo(pp);
-      acc_b = acc_b + bf_hi(pp);
+      if constexpr (KY == 2) {
+        acc[0] = acc[0] + bf_lo(pp);
+        acc[1] = acc[1] + bf_hi(pp);
+      } else if constexpr (KY == 4) {
+        acc[2 * (m & 1)] = acc[2 * (m & 1)] + bf_lo(pp);
+        acc[2 * (m & 1) + 1] = acc[2 * (m & 1) + 1] + bf_hi(pp);
+      } else {
+        acc[0] = acc[0] + bf_lo(pp);
+        acc[0] = acc[0] + bf_hi(pp);
+      }
     }
-    // Lower lanes hold accumulators 0, 1; upper lanes 2, 3 of the same candidate.
-    const float a01 = acc_a + acc_b;
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a01), __float_as_uint(a01), false, false);
-    const float ty = (__uint_as_float(sw[0]) + acc_a) + acc_b;  // valid in the upper lanes
+    float ty;
+    if constexpr (KY == 2) {
+      // Lower lanes hold accumulators 0, 1; upper lanes 2, 3 of the same thread.
+      const float a01 = acc[0] + acc[1];
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a01), __float_as_uint(a01), false, false);
+      ty = (__uint_as_float(sw[0]) + acc[0]) + acc[1];  // valid in the upper lanes
+    } else if constexpr (KY == 4) {
+      // Each lane half is one thread: t = ((a0 + a1) + a2) + a3; upper lanes add the
+      // lower half's (thread y) to their own (thread y + 2).
+      const float tt4 = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(tt4), __float_as_uint(tt4), false, false);
+      ty = __uint_as_float(sw[0]) + tt4;
+    } else {
+      // Wave 1 holds accumulators 0 (lower) and 1 (upper), wave 0 holds 2 and 3.
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0]), __float_as_uint(acc[0]), false, false);
+      ty = __uint_as_float(sw[0]) + acc[0];  // wave 1: a0 + a1
+      if (y == 0) t0val2 = acc[0];           // wave 0: a3 (a2 is sw[0], kept in t0val)
+      if (y == 0) ty = __uint_as_float(sw[0]);
+    }
     if (y == 1) {
       if (hf == 1) xbuf[((n & 1) * kTok + tl) * kTileC + col] = ty;
     } else {
@@ -537,7 +582,8 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
 //      after them, each in index order;
 //   3. stable two-pass radix sort of the picks on the key (descending), int64 out.
 struct SelParams {
-  const uint16_t* keys;  // [B*S, T]
+  const uint16_t* keys;  // [B*S, kstride], kstride = T rounded up to a multiple of 4
+  int64_t kstride;
   int64_t* out;          // [B*S, K]
   int32_t S, T, K, ratio, causal, psort;
   int64_t offset;
@@ -561,8 +607,8 @@ __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
   }
   const int K = p.K;
   const bool selecting = nv > K;
-  // Keys of this thread (8-byte loads: rows are 8-byte aligned since T % 4 == 0).
-  const uint2* src = reinterpret_cast<const uint2*>(p.keys + row * p.T) + 8 * tt;
+  // Keys of this thread (8-byte loads: rows start 8-byte aligned, kstride % 4 == 0).
+  const uint2* src = reinterpret_cast<const uint2*>(p.keys + row * p.kstride) + 8 * tt;
   const int c0 = 32 * tt;
   // Order keys are >= 0x007f (-inf), so 0 marks the positions past nv.
   uint2 kw[8];
@@ -667,7 +713,28 @@ __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
 // Called by the indexer entry points for h == 64, d == 128 (checks common to both
 // configurations are done by the caller).
 int64_t dsa_indexer_wide_workspace_bytes(int64_t b, int64_t s, int64_t n_cand) {
-  return b * s * n_cand * 2;  // one 16-bit order key per (token, candidate)
+  return b * s * ((n_cand + 3) & ~INT64_C(3)) * 2;  // a 16-bit order key per (token, candidate)
+}
+
+// The number of threads torch-ROCm's reduction kernel splits the 64 heads over when it
+// sums the bf16 [b, s, 64, T] products over the heads (reference/task2_v0_ref.py:134),
+// from its launch configuration for a reduction over a non-innermost dimension: the
+// output [b, s, T] is vectorised by 4 (T % 4 == 0), 2 (T % 2 == 0) or 1; a block
+// is min(pow2(N / vec), 64) threads wide (N = b s T outputs, 512 / vec threads in all)
+// and as many tall as fit, up to 64; the heads are split over the block's height only
+// when each of those threads still sums at least 16 of them. Measured on the MI355X
+// for T in 2 .. 8192 and N up to 132 K (T = 1, a single candidate, is reduced
+// differently, but its top-1 does not depend on the score).
+int torch_head_split(int64_t n_out, int64_t T) {
+  const int vec = (T % 4 == 0) ? 4 : (T % 2 == 0) ? 2 : 1;
+  const int64_t max_thr = 512 / vec;
+  const int64_t dim0 = n_out / vec;
+  int64_t p2 = 1;
+  while (p2 * 2 <= dim0 && p2 < max_thr) p2 *= 2;
+  const int64_t width = p2 < 64 ? p2 : 64;
+  int64_t height = max_thr / width;
+  if (height > 64) height = 64;
+  return (64 >= 16 * height) ? (int)height : 1;
 }
 
 // With a workspace of at least dsa_indexer_wide_workspace_bytes: the score kernel
@@ -680,10 +747,11 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
                             int64_t s, int64_t rd, int64_t n_cand, int64_t k_out,
                             int64_t ratio, int32_t causal, int64_t offset, void* workspace,
                             int64_t workspace_bytes, hipStream_t stream) {
-  // The head-sum order reproduced here is torch's for a candidate count that is a
-  // multiple of 4 (its reduction kernel vectorizes the output by 4 then).
-  if (n_cand > kMaxT || (n_cand % 4) != 0) return DSA_ERR_UNSUPPORTED;
+  if (n_cand > kMaxT) return DSA_ERR_UNSUPPORTED;
   if (k_out > kMaxK) return DSA_ERR_UNSUPPORTED;
+  // torch reduces a single candidate's heads another way; its score (not its top-1) differs.
+  if (scores != nullptr && n_cand == 1) return DSA_ERR_UNSUPPORTED;
+  const int ky = torch_head_split(b * s * n_cand, n_cand);
   const bool two_pass = scores == nullptr && workspace != nullptr &&
                         workspace_bytes >= dsa_indexer_wide_workspace_bytes(b, s, n_cand);
   if (workspace != nullptr && ((uintptr_t)workspace & 15u)) return DSA_ERR_ALIGN;
@@ -698,6 +766,7 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
   p.out = out;
   p.gkeys = scores != nullptr ? scores : (two_pass ? (uint16_t*)workspace : nullptr);
   p.graw = scores != nullptr ? 1 : 0;
+  p.gstride = scores != nullptr ? n_cand : ((n_cand + 3) & ~INT64_C(3));
   p.B = (int32_t)b;
   p.S = (int32_t)s;
   p.rd = (int32_t)rd;
@@ -739,18 +808,24 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
   }
   if (smem > 160 * 1024) return DSA_ERR_UNSUPPORTED;
   const bool fused = p.gkeys == nullptr;
-  const void* kfn = fused ? (const void*)ix_wide_kernel<true> : (const void*)ix_wide_kernel<false>;
+  const void* kfns[2][3] = {
+      {(const void*)ix_wide_kernel<false, 1>, (const void*)ix_wide_kernel<false, 2>,
+       (const void*)ix_wide_kernel<false, 4>},
+      {(const void*)ix_wide_kernel<true, 1>, (const void*)ix_wide_kernel<true, 2>,
+       (const void*)ix_wide_kernel<true, 4>}};
+  const int kyi = ky == 1 ? 0 : ky == 2 ? 1 : 2;
+  const void* kfn = kfns[fused ? 1 : 0][kyi];
   if (dsa_host::ensure_dyn_lds(kfn, (int)smem) != DSA_OK) return DSA_ERR_LAUNCH;
   const int64_t blocks = b * p.groups * (int64_t)p.csplit;
   if (blocks > INT32_MAX || b * s > INT32_MAX) return DSA_ERR_SHAPE;
-  if (fused)
-    hipLaunchKernelGGL(ix_wide_kernel<true>, dim3((unsigned)blocks), dim3(512), smem, stream, p);
-  else
-    hipLaunchKernelGGL(ix_wide_kernel<false>, dim3((unsigned)blocks), dim3(512), smem, stream, p);
+  void* kargs[] = {&p};
+  if (hipLaunchKernel(kfn, dim3((unsigned)blocks), dim3(512), kargs, smem, stream) != hipSuccess)
+    return DSA_ERR_LAUNCH;
   if (hipGetLastError() != hipSuccess) return DSA_ERR_LAUNCH;
   if (two_pass) {
     SelParams sp;
     sp.keys = (const uint16_t*)workspace;
+    sp.kstride = p.gstride;
     sp.out = out;
     sp.S = p.S;
     sp.T = p.T;

@@ -194,8 +194,9 @@ int dsa_indexer_rope(void* q, const void* freqs_cis, int64_t b, int64_t s, int64
  * Requirements: rd as for dsa_indexer_rope (when freqs_cis != NULL), ratio >= 1,
  * 1 <= k_out <= n_cand, and one of
  *   h == 16, d == 64:   n_cand <= 2048, k_out <= 256                (configs[2])
- *   h == 64, d == 128:  n_cand <= 8192, n_cand % 4 == 0, k_out <= 2048 (configs[4]; the
- *                       head-sum order reproduced is torch's for n_cand % 4 == 0)
+ *   h == 64, d == 128:  n_cand <= 8192, k_out <= 2048 (configs[4]; the 64-head sum is
+ *                       added in the order torch-ROCm's reduction uses for b*s*n_cand
+ *                       outputs of n_cand candidates: over 1, 2 or 4 threads)
  */
 int dsa_indexer_score_topk(const void* q, const void* kv_cache, int64_t kv_batch_stride,
                            const void* wl, float w_scale, const void* freqs_cis,
@@ -205,8 +206,8 @@ int dsa_indexer_score_topk(const void* q, const void* kv_cache, int64_t kv_batch
 
 /*
  * Workspace for dsa_indexer_score_topk_ws, in bytes (0: the configuration needs none;
- * DSA_ERR_SHAPE: invalid sizes). For h == 64, d == 128 it is b * s * n_cand * 2 (one 16-bit order
- * key per token and candidate).
+ * DSA_ERR_SHAPE: invalid sizes). For h == 64, d == 128 it is b * s * round_up(n_cand, 4) * 2
+ * (one 16-bit order key per token and candidate, rows padded to 8 bytes).
  */
 int64_t dsa_indexer_workspace_bytes(int64_t b, int64_t s, int64_t h, int64_t d, int64_t n_cand);
 
@@ -232,7 +233,7 @@ int dsa_indexer_score_topk_ws(const void* q, const void* kv_cache, int64_t kv_ba
  * library (one per device, held from module load until the process ends). Same
  * arguments and results as dsa_indexer_score_topk. Returns DSA_ERR_SCRATCH when
  * dsa_indexer_workspace_bytes(b, s, h, d, n_cand) exceeds that size (64 heads x 128:
- * b * s * n_cand <= 8,388,608, e.g. 1024 tokens at 8192 candidates); configurations
+ * b * s * round_up(n_cand, 4) <= 8,388,608, e.g. 1024 tokens at 8192 candidates); configurations
  * that need no workspace (16 heads x 64) run as dsa_indexer_score_topk. Calls on one
  * device share the array, so calls that overlap on one device (different streams)
  * race; calls ordered on one stream do not. No hipMalloc/hipFree or other allocating
@@ -252,8 +253,9 @@ int dsa_indexer_score_topk_noalloc(const void* q, const void* kv_cache, int64_t 
 /*
  * Task2 score stage alone: writes the bf16 index_score [b, s, n_cand] that the reference
  * hands to topk (reference/task2_v0_ref.py:131-137), with masked entries = -inf in the
- * causal case. Same arguments and requirements as dsa_indexer_score_topk; `scores` is a
- * device buffer of b*s*n_cand bf16 words. Used to check the rounding chain stage by stage
+ * causal case. Same arguments and requirements as dsa_indexer_score_topk (and, for
+ * h == 64, n_cand >= 2: torch reduces a single candidate's heads in another order);
+ * `scores` is a device buffer of b*s*n_cand bf16 words. Used to check the rounding chain stage by stage
  * and by callers that want the scores themselves.
  */
 int dsa_indexer_scores(const void* q, const void* kv_cache, int64_t kv_batch_stride,

@@ -16,9 +16,12 @@ HIP kernel against the same rules.
                                re = fma(-b, d, a*c),  im = (a*d) + (b*c)
   head_sum        fp32 sum over the heads (task2_v0_ref.py:134): 'rocm' = four running
                   accumulators over heads j, j+4, j+8, j+12, combined ((a0+a1)+a2)+a3
-                  (16 heads); 'rocm_split2' = that over the even and over the odd heads,
-                  then even + odd (64 heads, candidate count % 4 == 0); 'seq' = one
-                  accumulator in head order
+                  (16 heads; 64 heads when torch does not split them); 'rocm_split2' =
+                  that over the even and over the odd heads, then even + odd;
+                  'rocm_split4' = that over heads y, y+4, ... for y = 0..3, then
+                  (t0 + t2) + (t1 + t3); 'seq' = one accumulator in head order
+  torch_head_split  how many threads torch-ROCm's reduction kernel splits 64 heads over
+                  (1, 2 or 4) for a candidate count T and N = b*s*T outputs
   score_chain     bf16(head_sum(bf16(relu(bf16(S)) * w)))
   topk_order      indices of the k largest bf16 values, value descending then index
                   ascending (a stable order); -1/offset fill of task2_v0_ref.py:139-143
@@ -93,8 +96,11 @@ def head_sum(v, order: str = "rocm") -> np.ndarray:
                   ((a0+a1)+a2)+a3 (torch-ROCm's reduction of a short middle dimension,
                   e.g. 16 heads);
     'rocm_split2' two threads over the even and the odd heads, each as 'rocm' over its
-                  heads (accumulator i of thread y: heads y+2i+8m), then even + odd
-                  (torch-ROCm for 64 heads with a candidate count divisible by 4);
+                  heads (accumulator i of thread y: heads y+2i+8m), then even + odd;
+    'rocm_split4' four threads over heads y, y+4, ..., each as 'rocm' over its heads,
+                  then (t0 + t2) + (t1 + t3) (torch-ROCm's halving tree);
+                  for 64 heads torch_head_split says which of 'rocm' (1 thread),
+                  'rocm_split2' and 'rocm_split4' torch uses;
     'seq'         one accumulator in head order."""
     v = np.asarray(v, np.float32)
     if order == "rocm_split2":
@@ -103,6 +109,11 @@ def head_sum(v, order: str = "rocm") -> np.ndarray:
         even = head_sum(v[..., 0::2], "rocm")
         odd = head_sum(v[..., 1::2], "rocm")
         return (even + odd).astype(np.float32)
+    if order == "rocm_split4":
+        if v.shape[-1] % 16:
+            raise ValueError(order)
+        t = [head_sum(v[..., y::4], "rocm") for y in range(4)]
+        return ((t[0] + t[2]).astype(np.float32) + (t[1] + t[3]).astype(np.float32)).astype(np.float32)
     if order == "seq":
         acc = np.zeros(v.shape[:-1], np.float32)
         for i in range(v.shape[-1]):
@@ -117,6 +128,27 @@ def head_sum(v, order: str = "rocm") -> np.ndarray:
             acc = (acc + v[..., i]).astype(np.float32)
         accs.append(acc)
     return (((accs[0] + accs[1]).astype(np.float32) + accs[2]).astype(np.float32) + accs[3]).astype(np.float32)
+
+
+def torch_head_split(n_out: int, t: int) -> int:
+    """Threads over which torch-ROCm's reduction kernel splits a 64-long middle dimension
+    (x[b, s, 64, T].sum(dim=2), N = b*s*T outputs): the output is vectorised by 4, 2 or 1
+    (the largest that divides T); a block is min(pow2(N / vec), 64) threads wide out of
+    512 / vec, as tall as fits (at most 64), and the heads are split over its height only
+    if each thread keeps at least 16 of them. T = 1 is reduced along another path."""
+    vec = 4 if t % 4 == 0 else 2 if t % 2 == 0 else 1
+    max_thr = 512 // vec
+    dim0 = n_out // vec
+    p2 = 1
+    while p2 * 2 <= dim0 and p2 < max_thr:
+        p2 *= 2
+    height = min(64, max_thr // min(p2, 64))
+    return height if 64 >= 16 * height else 1
+
+
+def head_sum_order_64(n_out: int, t: int) -> str:
+    """head_sum order name of torch-ROCm's 64-head sum for (N, T)."""
+    return {1: "rocm", 2: "rocm_split2", 4: "rocm_split4"}[torch_head_split(n_out, t)]
 
 
 def score_chain(s_bits, w_bits, order: str = "rocm") -> np.ndarray:

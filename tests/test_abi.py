@@ -185,7 +185,6 @@ def _ixw(lib, **kw):
 def test_wide_indexer_host_checks():
     lib = _native.load()
     assert _ixw(lib, T=8196, kvbs=8196 * 128) == -3  # more than 8192 candidates
-    assert _ixw(lib, T=8190, kvbs=8190 * 128) == -3  # candidate count not a multiple of 4
     assert _ixw(lib, T=8192, K=4096) == -3           # top-k beyond 2048
     assert _ixw(lib, K=8193) == -2                   # k > candidates
     assert _ixw(lib, kvbs=100) == -2
@@ -200,6 +199,7 @@ def test_workspace_bytes():
     lib = _native.load()
     assert lib.dsa_indexer_workspace_bytes(1, 8192, 64, 128, 8192) == 8192 * 8192 * 2
     assert lib.dsa_indexer_workspace_bytes(2, 100, 64, 128, 512) == 2 * 100 * 512 * 2
+    assert lib.dsa_indexer_workspace_bytes(1, 3, 64, 128, 8190) == 3 * 8192 * 2   # rows padded to 4 keys
     assert lib.dsa_indexer_workspace_bytes(8, 2600, 16, 64, 650) == 0   # the 16-head kernel needs none
     assert lib.dsa_indexer_workspace_bytes(-1, 8, 64, 128, 64) == -2
 

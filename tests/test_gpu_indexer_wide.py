@@ -29,6 +29,34 @@ def _wide_bits(shape, g):
     return ((sgn << 15) | (ex << 7) | mn).to(torch.int16).view(torch.bfloat16)
 
 
+def _cancelling_bits(shape, g):
+    """Small N(0,1) values plus eight exactly cancelling pairs of large values per output:
+    every summation order of the heads rounds differently."""
+    b, s_, h, t = shape
+    x = torch.randn(shape, generator=g)
+    perm = torch.argsort(torch.rand(b, s_, t, h, generator=g), dim=-1)
+    big = torch.exp2(torch.randint(14, 21, (b, s_, t, 8), generator=g).float()) * (
+        1 + torch.randint(0, 128, (b, s_, t, 8), generator=g).float() / 128)
+    xt = x.permute(0, 1, 3, 2).contiguous()
+    xt.scatter_(-1, perm[..., :8], big)
+    xt.scatter_(-1, perm[..., 8:16], -big)
+    return xt.permute(0, 1, 3, 2).contiguous().to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("b,s,t", [(1, 1, 128), (1, 1, 64), (2, 3, 130), (1, 7, 1001), (1, 40, 8190),
+                                   (1, 1, 8189), (1, 2, 8192), (3, 5, 258), (1, 1, 66)])
+def test_torch_head_sum_rule_64_all_splits(gpu, b, s, t):
+    """torch-ROCm's x[b, s, 64, T].sum(dim=2) equals head_sum in the order rules.torch_head_split
+    names (1, 2 or 4 threads) at shapes of each kind."""
+    g = torch.Generator().manual_seed(b * 100000 + s * 10000 + t)
+    x = _cancelling_bits((b, s, 64, t), g)
+    order = rules.head_sum_order_64(b * s * t, t)
+    _say("rule head-sum 64", (b, s, t), order)
+    got = bits_of(x.to(gpu).sum(dim=2))
+    want = rules.bf16_round(rules.head_sum(np.moveaxis(rules.bf16_to_f32(bits_of(x)), 2, -1), order))
+    assert np.array_equal(got, want), int((got != want).sum())
+
+
 def test_torch_head_sum_rule_64(gpu):
     """x[1, 512, 64, 1024].sum(dim=2): two threads (even / odd heads), four accumulators each."""
     g = torch.Generator().manual_seed(11)
@@ -74,7 +102,11 @@ def _check_equal(got, want, name):
     assert eq, name
 
 
-@pytest.mark.parametrize("seqlen,start_pos", [(512, 0), (96, 0), (64, 128)])
+@pytest.mark.parametrize("seqlen,start_pos", [(512, 0), (96, 0), (64, 128),
+                                              # candidate counts of every head-split kind:
+                                              # T = 1001 (1 thread), 130 (4), 128 with one
+                                              # token (4), 64 with one token (1), 1002 (4)
+                                              (1001, 0), (3, 127), (1, 127), (1, 63), (1002, 0)])
 def test_wide_score_stage_matches_torch(gpu, seqlen, start_pos):
     args = _args(start_pos + seqlen, 2048)
     m, r = _pair(args, 31, start_pos + seqlen, 1, gpu, wstd=0.02)
@@ -111,6 +143,22 @@ WIDE = [
     (1, 8191, 2, 2048, 1),
     (16, 4000, 0, 512, 1),
     (2, 3006, 1, 256, 2),
+    # candidate counts that are not multiples of 4, and few outputs, where torch sums the
+    # 64 heads over 1 or 4 threads instead of 2: decode one token at T = 8189 (odd),
+    # 8190 (T % 4 == 2), 8191; two tokens at 8191; prefill of odd and 2-mod-4 lengths;
+    # one token at T = 128 (4 threads) and T = 64 (1 thread); ratio 2 with T = 1502
+    (1, 8188, 0, 2048, 1),
+    (1, 8189, 3, 2048, 1),
+    (1, 8190, 0, 2048, 1),
+    (2, 8189, 0, 2048, 1),
+    (1001, 0, 0, 2048, 1),
+    (1002, 0, 4, 512, 1),
+    (255, 0, 0, 100, 1),
+    (1, 127, 0, 64, 1),
+    (1, 63, 0, 32, 1),
+    (1, 3004, 0, 1024, 2),
+    (2, 1, 0, 3, 1),      # T = 3
+    (1, 0, 0, 1, 1),      # T = 1: a single candidate (top-1 whatever its score)
 ]
 
 

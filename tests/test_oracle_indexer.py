@@ -185,6 +185,55 @@ def test_head_sum_split2_rule():
     assert not np.array_equal(s2, rules.head_sum(w, "rocm"))
 
 
+def _thread_tree_sum(v, y_threads):
+    """Torch-ROCm's reduction as an algorithm, one output at a time: thread y of Y adds heads
+    y, y + Y, ... into accumulator j % 4 (its j-th head), combines ((a0 + a1) + a2) + a3,
+    and the thread totals are added in a halving tree (stride Y/2, Y/4, ...)."""
+    out = np.zeros(v.shape[0], np.float32)
+    for r in range(v.shape[0]):
+        tot = []
+        for y in range(y_threads):
+            acc = [np.float32(0)] * 4
+            for j, h in enumerate(range(y, v.shape[1], y_threads)):
+                acc[j % 4] = np.float32(acc[j % 4] + v[r, h])
+            tot.append(np.float32(np.float32(np.float32(acc[0] + acc[1]) + acc[2]) + acc[3]))
+        off = y_threads // 2
+        while off:
+            for y in range(off):
+                tot[y] = np.float32(tot[y] + tot[y + off])
+            off //= 2
+        out[r] = tot[0]
+    return out
+
+
+def test_head_sum_split_orders_match_thread_simulation():
+    """head_sum's 'rocm' / 'rocm_split2' / 'rocm_split4' (vectorised numpy) equal the
+    thread-by-thread statement of the reduction for 1, 2 and 4 threads, on data where the
+    orders differ from each other."""
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((300, 64)) * np.exp2(rng.integers(-12, 12, (300, 64)))).astype(np.float32)
+    got = {}
+    for y, order in ((1, "rocm"), (2, "rocm_split2"), (4, "rocm_split4")):
+        got[order] = rules.head_sum(w, order)
+        assert np.array_equal(got[order], _thread_tree_sum(w, y)), order
+    assert not np.array_equal(got["rocm"], got["rocm_split2"])
+    assert not np.array_equal(got["rocm_split2"], got["rocm_split4"])
+    assert not np.array_equal(got["rocm"], got["rocm_split4"])
+
+
+def test_torch_head_split_matches_measured_table():
+    """rules.torch_head_split (the thread count of torch-ROCm's 64-head sum) against the
+    table measured on the MI355X by tests/golden/measure_torch_head_split.py (N = s*T
+    outputs up to 132 K, T = 2 .. 8192): for every measured shape exactly one order matched
+    all outputs, and it is the one the rule names."""
+    f = np.load(os.path.join(GOLDEN, "torch_head_split.npz"))
+    assert (f["y"] > 0).all()
+    pred = np.array([rules.torch_head_split(int(n), int(t)) for n, t in zip(f["n_out"], f["t"])])
+    bad = np.nonzero(pred != f["y"])[0]
+    assert len(bad) == 0, [(int(f["n_out"][i]), int(f["t"][i]), int(f["y"][i]), int(pred[i])) for i in bad[:5]]
+    assert set(f["y"].tolist()) == {1, 2, 4}
+
+
 def test_freqs_cis_matches_reference_table():
     """precompute_freqs_cis (oracle and product) against the RoPE table the reference's own
     get_init_inputs builds (task2_v0_ref.py:162-172; fixture written by importing it): the
