@@ -39,6 +39,7 @@ EXPORTS = (
     "dsa_indexer_score_topk_ws",
     "dsa_indexer_score_topk_noalloc",
     "dsa_indexer_scores",
+    "dsa_indexer_q_proj",
 )
 
 _c_i64 = ctypes.c_int64
@@ -120,6 +121,9 @@ def load() -> ctypes.CDLL:
     lib.dsa_indexer_scores.argtypes = [
         _c_vp, _c_vp, _c_i64, _c_vp, ctypes.c_float, _c_vp, ctypes.c_int32, _c_vp,
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32, _c_vp]
+    lib.dsa_indexer_q_proj.restype = ctypes.c_int
+    lib.dsa_indexer_q_proj.argtypes = [
+        _c_vp, _c_vp, _c_vp, ctypes.c_int32, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]
     v = lib.dsa_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {v}, expected {ABI_VERSION}")
@@ -311,4 +315,29 @@ def indexer_scores(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor, w_
         fr.data_ptr() if fr is not None else None, int(rope_mode), out.data_ptr(),
         b, s, h, d, rope_head_dim, n_cand, ratio, 1 if causal else 0, _stream(q))
     _check("dsa_indexer_scores", rc)
+    return out
+
+
+def indexer_q_proj(qr: torch.Tensor, weight: torch.Tensor, freqs_cis: Optional[torch.Tensor],
+                   head_dim: int, rope_head_dim: int,
+                   rope_mode: int = DSA_ROPE_TORCH_ROCM) -> torch.Tensor:
+    """q = qr . weight^T as bf16 [b, s, n/head_dim, head_dim] (F.linear's rounding), with
+    RoPE on the last rope_head_dim channels of every head when freqs_cis (rows for the s
+    positions) is given. qr: bf16 [b, s, k]; weight: bf16 [n, k]."""
+    lib = load()
+    if qr.dim() != 3 or weight.dim() != 2 or qr.shape[2] != weight.shape[1]:
+        raise ValueError(f"qr {tuple(qr.shape)} and weight {tuple(weight.shape)} do not match")
+    if qr.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("qr and weight must be bfloat16")
+    b, s, k = qr.shape
+    n = weight.shape[0]
+    qr = qr.contiguous()
+    weight = weight.contiguous()
+    fr = _freqs_view(freqs_cis, s, rope_head_dim) if freqs_cis is not None else None
+    _require_gpu(qr, weight, *([fr] if fr is not None else []))
+    out = torch.empty(b, s, n // head_dim, head_dim, dtype=torch.bfloat16, device=qr.device)
+    rc = lib.dsa_indexer_q_proj(qr.data_ptr(), weight.data_ptr(), fr.data_ptr() if fr is not None else None,
+                                int(rope_mode), out.data_ptr(), b * s, n, k, head_dim, rope_head_dim,
+                                max(s, 1), _stream(qr))
+    _check("dsa_indexer_q_proj", rc)
     return out

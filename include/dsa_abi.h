@@ -263,6 +263,30 @@ int dsa_indexer_scores(const void* q, const void* kv_cache, int64_t kv_batch_str
                        void* scores, int64_t b, int64_t s, int64_t h, int64_t d, int64_t rd,
                        int64_t n_cand, int64_t ratio, int32_t causal, void* stream);
 
+/*
+ * Task2 query projection with RoPE: q = qr . wq^T (the F.linear of the indexer's wq_b,
+ * reference/task2_v0_ref.py:129-130 through Linear.forward :81-83) followed by
+ * apply_rotary_emb on the last rd channels of every head (:131, :93-104), as one kernel.
+ * The product accumulates in fp32 over k in ascending order and rounds once to bf16,
+ * which equals torch-ROCm's F.linear at the indexer's shapes for the token counts its
+ * GPU test covers (not for every small m: hipBLASLt reduces those in another order).
+ *
+ *   qr         bf16 [m, k]        m = b * s_len token rows
+ *   wq         bf16 [n, k]        n = heads * head_dim
+ *   freqs_cis  complex64 [s_len, rd/2] rows of positions start_pos .. (16-byte aligned), or
+ *              NULL for no RoPE
+ *   rope_mode  DSA_ROPE_TORCH_ROCM or DSA_ROPE_CPU, the rounding rule of the rotation (as for
+ *              dsa_indexer_score_topk)
+ *   q          bf16 [m, n] output
+ * Requirements: k % 32 == 0, n % 256 == 0, head_dim in {64, 128}, (head_dim - rd) % 8 == 0,
+ * m * k * 2 and n * k * 2 below 2^32, m % s_len == 0; pointers 16-byte aligned.
+ * The drop-in Model keeps F.linear + the score kernel's own RoPE: at configs[2] this kernel
+ * is not faster than hipBLASLt.
+ */
+int dsa_indexer_q_proj(const void* qr, const void* wq, const void* freqs_cis, int32_t rope_mode,
+                       void* q, int64_t m, int64_t n, int64_t k, int64_t head_dim, int64_t rd,
+                       int64_t s_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -235,3 +235,24 @@ def test_indexer_noalloc_host_checks():
     assert f(b=-1) == -2
     assert f(out=None) == -1
     assert f(s=0) == 0
+
+
+def test_q_proj_host_checks():
+    lib = _native.load()
+
+    def f(**kw):
+        a = dict(qr=16, w=16, fr=16, mode=1, q=16, m=2600, n=1024, k=256, d=64, rd=32, s=2600)
+        a.update(kw)
+        return lib.dsa_indexer_q_proj(a["qr"], a["w"], a["fr"], a["mode"], a["q"], a["m"], a["n"], a["k"],
+                                      a["d"], a["rd"], a["s"], None)
+
+    assert f(m=-1) == -2
+    assert f(k=250) == -3          # k % 32
+    assert f(n=1000, d=40) == -3   # n % 256
+    assert f(rd=30) == -3          # rotated channels not on an 8-channel boundary
+    assert f(rd=66) == -2          # rd > head_dim
+    assert f(m=2599) == -2         # m not a multiple of s_len
+    assert f(mode=5) == -3
+    assert f(m=0) == 0
+    assert f(q=None) == -1
+    assert f(fr=24) == -6          # table not 16-byte aligned
