@@ -128,7 +128,9 @@ __device__ __forceinline__ int find_bin(const uint32_t* hist, int lane, uint32_t
   return hm ? b : -1;
 }
 
-template <int E>
+// kDump: the bf16 scores are written to p.scores (the score-stage entry point);
+// the top-k build carries no dump code in its tile loop.
+template <int E, bool kDump>
 __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int KP = 32 * E;  // sort size per half-wave
@@ -149,9 +151,7 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   unsigned char* wbase = smem + (size_t)wi * p.wave_bytes;
   uint16_t* keys = reinterpret_cast<uint16_t*>(wbase) ;                // [2][NT][32]
   uint32_t* hist = reinterpret_cast<uint32_t*>(wbase + p.keys_bytes);   // [2][256]
-  uint32_t* sbuf = hist + 512;                                         // [2][KP]
   uint32_t* myhist = hist + 256 * half;
-  uint32_t* mysbuf = sbuf + KP * half;
 
   const int nv = n_valid(p, t);
   // Tiles of the workgroup: up to the valid candidates of its last token (the
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   const int tg_last = min(2 * (4 * grp + 3) + 1, p.S - 1);
   const int ntile = (n_valid(p, tg_last) + 31) >> 5;
   const int ntile_all = (p.keys_bytes / 128);
-  // Candidate tiles (32 rows x 128 B) in a 4-slot LDS ring after the wave areas.
+  // Candidate tiles (32 rows x 128 B) in a 3-slot LDS ring after the wave areas.
   uint8_t* ring = smem + 4 * (size_t)p.wave_bytes;
 
   // Head weights of this half's token, bf16(fp32(wl) * w_scale), fp32 copies.
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   *reinterpret_cast<u32x4*>(myhist + 8 * hl + 4) = u32x4{0u, 0u, 0u, 0u};
   lds_fence();
 
-  // Tile n is copied by buffer_load ... lds into ring slot n % 4: wave wi moves rows
+  // Tile n is copied by buffer_load ... lds into ring slot n % 3: wave wi moves rows
   // 8wi .. 8wi+7 (lane l: row 8wi + l/8, 16-byte chunk (l%8) ^ (row%8), so chunk c of
   // row r sits at position 8r + (c ^ (r%8)) and the fragment reads below spread over
   // all banks). Rows >= T read as zero through the resource's range.
@@ -230,12 +230,12 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   const int wis = __builtin_amdgcn_readfirstlane(wi);
   const int crow = 8 * wis + (lane >> 3);
   const uint32_t coff = (uint32_t)(crow * kD + 8 * ((lane & 7) ^ (crow & 7))) * 2u;
-  auto issue = [&](int n) {
-    lds_dma16(krs, (uint32_t)(32 * n * kD * 2) + coff, ring_lds + 4096u * (uint32_t)(n & 3) + 1024u * (uint32_t)wis);
+  auto issue = [&](int n, int slot) {
+    lds_dma16(krs, (uint32_t)(32 * n * kD * 2) + coff, ring_lds + 4096u * (uint32_t)slot + 1024u * (uint32_t)wis);
   };
 #pragma unroll
-  for (int j = 0; j < 3; ++j)
-    if (j < ntile) issue(j);
+  for (int j = 0; j < 2; ++j)
+    if (j < ntile) issue(j, j);
   // Consume the compiler-tracked loads here: its own vmcnt(0) for them (which also
   // covers the copies just issued) then stays out of the loop.
 #pragma unroll
@@ -245,13 +245,15 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   // B operand: candidate 32*tile + lane%32, channels 16ks + 8(lane/32) .. +7.
   const int kcol = lane & 31;
   const int khalf = lane >> 5;
+  int slot = 0;  // tile % 3
   for (int tile = 0; tile < ntile; ++tile) {
-    if (tile + 2 < ntile) wait_vmcnt<2>();
-    else if (tile + 1 < ntile) wait_vmcnt<1>();
+    if (tile + 1 < ntile) wait_vmcnt<1>();
     else wait_vmcnt<0>();
     __syncthreads();  // tile `tile` is in LDS for every wave; the slot of tile-1 is free
-    if (tile + 3 < ntile) issue(tile + 3);
-    const u32x4* kt = reinterpret_cast<const u32x4*>(ring + 4096 * (tile & 3));
+    const int slot_next = slot == 0 ? 2 : slot - 1;  // (tile + 2) % 3 == (tile - 1) % 3
+    if (tile + 2 < ntile) issue(tile + 2, slot_next);
+    const u32x4* kt = reinterpret_cast<const u32x4*>(ring + 4096 * slot);
+    slot = slot == 2 ? 0 : slot + 1;
     f32x16 acc = {};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -286,29 +288,43 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
       v[r + 1] = bf_hi(pb);
     }
     // Head j is in slot j (j<4), j+4 -> slot j+8, j+8 -> slot j+4, j+12 -> slot j+12;
-    // IEEE fp32 adds in torch's order.
+    // IEEE fp32 adds in torch's order. torch's four accumulators start at +0; adding
+    // the +0 once to the total instead gives the same value (x + 0 == x except for
+    // the sign of a zero, and a -0 can only reach the total when every term is -0).
     float a4[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a4[j] = (((0.0f + v[j]) + v[j + 8]) + v[j + 4]) + v[j + 12];
-    const float tot = ((a4[0] + a4[1]) + a4[2]) + a4[3];
+    for (int j = 0; j < 4; ++j) a4[j] = ((v[j] + v[j + 8]) + v[j + 4]) + v[j + 12];
+    const float tot = (((a4[0] + a4[1]) + a4[2]) + a4[3]) + 0.0f;
     uint16_t sc = f2bf(tot);
     const int c = 32 * tile + hl;
     const bool valid = c < nv;
-    if (p.causal) sc = f2bf(bf2f(sc) + 0.0f);  // the reference adds the 0/-inf mask
+    // The reference adds the 0/-inf mask: bf16(x + 0) turns -0 into +0, nothing else.
+    if (p.causal && sc == 0x8000u) sc = 0;
     uint16_t u = (uint16_t)(sc ^ ((sc & 0x8000u) ? 0xffffu : 0x8000u));
-    if ((sc & 0x7fffu) > 0x7f80u) u = 0xffffu;  // NaN ranks above everything
+    if (__builtin_isnan(tot)) u = 0xffffu;  // NaN ranks above everything
     keys[(half * ntile_all + tile) * 32 + hl] = valid ? u : (uint16_t)0;
-    if (p.scores != nullptr && t < p.S && c < p.T)
-      p.scores[((int64_t)b * p.S + t) * p.T + c] = valid ? sc : (uint16_t)0xff80u;
+    if constexpr (kDump) {
+      if (t < p.S && c < p.T)
+        p.scores[((int64_t)b * p.S + t) * p.T + c] = valid ? sc : (uint16_t)0xff80u;
+    }
     if (valid) atomicAdd(&myhist[u >> 8], 1u);
   }
-  if (p.out == nullptr) {  // score dump only: fill the never-valid tail with -inf
+  if constexpr (kDump) {  // score dump only: fill the never-valid tail with -inf
     if (t < p.S)
       for (int c = 32 * ntile + hl; c < p.T; c += 32)
         p.scores[((int64_t)b * p.S + t) * p.T + c] = (uint16_t)0xff80u;
     return;
   }
   lds_fence();
+
+  // The picks of the select go to ring slots no wave reads any more: every wave
+  // has passed the barrier of the last tile, so only the last tile's slot may
+  // still be read; the other two held tiles whose reads and copies are done
+  // (256 E bytes per wave; E = 8 takes both slots).
+  constexpr int kWavesPerSlot = (16 / E) < 4 ? (16 / E) : 4;
+  const int sslot = (((ntile > 0 ? ntile - 1 : 0) + 1 + wi / kWavesPerSlot) % 3);
+  uint32_t* mysbuf = reinterpret_cast<uint32_t*>(ring + 4096 * sslot + (wi % kWavesPerSlot) * (256 * E)) +
+                     KP * half;
 
   // The reference ranks all T candidates; masked ones carry -inf (order key
   // 0x007f). Their count is known, so they enter the histograms analytically.
@@ -554,17 +570,25 @@ int launch_ix(const void* q, const void* kv_cache, int64_t kv_batch_stride, cons
   p.keys_bytes = ntile * 128;  // 2 halves x 32 lanes x uint16 per tile
   int E = 1;
   while (32 * E < k_out) E <<= 1;
-  p.wave_bytes = p.keys_bytes + 2048 + 8 * 32 * E;
-  const size_t smem = (size_t)p.wave_bytes * 4 + 4 * 4096;  // 4 wave areas + the tile ring
+  // Per wave: its key rows and two 256-bin histograms; then the 3-slot tile ring,
+  // which also holds the picks after the tile loop (256 E bytes per wave). At
+  // configs[2] (T 650, k 128) this is 31,232 bytes: five workgroups per CU.
+  p.wave_bytes = p.keys_bytes + 2048;
+  const size_t smem = (size_t)p.wave_bytes * 4 + 3 * 4096;
   if (smem > 64 * 1024) return DSA_ERR_UNSUPPORTED;
   const int64_t blocks = (int64_t)b * ((p.npairs + 3) / 4);  // 4 token pairs of one batch each
   if (blocks > INT32_MAX) return DSA_ERR_SHAPE;
   hipStream_t st = (hipStream_t)stream;
+  if (scores != nullptr) {  // score stage: out == nullptr, k == 1
+    if (out != nullptr || E != 1) return DSA_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((ix_score_topk_kernel<1, true>), dim3((unsigned)blocks), dim3(256), smem, st, p);
+    return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+  }
   switch (E) {
-    case 1: hipLaunchKernelGGL(ix_score_topk_kernel<1>, dim3((unsigned)blocks), dim3(256), smem, st, p); break;
-    case 2: hipLaunchKernelGGL(ix_score_topk_kernel<2>, dim3((unsigned)blocks), dim3(256), smem, st, p); break;
-    case 4: hipLaunchKernelGGL(ix_score_topk_kernel<4>, dim3((unsigned)blocks), dim3(256), smem, st, p); break;
-    case 8: hipLaunchKernelGGL(ix_score_topk_kernel<8>, dim3((unsigned)blocks), dim3(256), smem, st, p); break;
+    case 1: hipLaunchKernelGGL((ix_score_topk_kernel<1, false>), dim3((unsigned)blocks), dim3(256), smem, st, p); break;
+    case 2: hipLaunchKernelGGL((ix_score_topk_kernel<2, false>), dim3((unsigned)blocks), dim3(256), smem, st, p); break;
+    case 4: hipLaunchKernelGGL((ix_score_topk_kernel<4, false>), dim3((unsigned)blocks), dim3(256), smem, st, p); break;
+    case 8: hipLaunchKernelGGL((ix_score_topk_kernel<8, false>), dim3((unsigned)blocks), dim3(256), smem, st, p); break;
     default: return DSA_ERR_UNSUPPORTED;
   }
   return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
