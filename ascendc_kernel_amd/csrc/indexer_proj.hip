@@ -187,6 +187,302 @@ __global__ __launch_bounds__(256) void ix_proj_kernel(ProjParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// k = 256 (the configs[2] wq_b): W-stationary persistent kernel.
+//
+// With k = 256 a wave's share of W (64 channels x 256 k, 32 KB) fits in 128
+// VGPRs as the A operand of all 16 k-steps, so W is read from L2 once per wave
+// and only the token side streams. Workgroup = 4 waves = 256 channels; two
+// workgroups per CU. A workgroup walks a contiguous run of 32-token tiles: each
+// tile's qr rows (16 KB) and, with RoPE, the tile's table rows (32 x rd/2
+// complex) are copied by buffer_load ... lds into a 3-slot ring two tiles ahead;
+// a wave computes q^T[64 ch x 32 tok] with 2 x 16 mfma 32x32x16 (k ascending, as
+// the streaming kernel above), rounds, rotates, and writes its 32 x 128-byte row
+// pieces through a wave-private LDS transpose with buffer stores (rows past M
+// are dropped by the range check, so every wave issues the same number of
+// vector-memory operations per tile, which the explicit waits count).
+// The workgroups that share a token run (one per 256-channel group) are given
+// ids on the same XCD, so the run's qr rows come from HBM once.
+
+constexpr int kSK = 256;                       // k of this kernel
+constexpr int kSTok = 32;                      // tokens per tile
+constexpr int kSCh = 256;                      // channels per workgroup
+constexpr int kSRing = 3;
+constexpr int kSXUnits = kSTok * kSK * 2 / 1024;  // 16 copy units of 1 KB (qr rows)
+constexpr int kSStoresW = 4;                   // 16-byte stores per lane and tile
+constexpr int kSStageBytes = 4 * kSTok * 128;  // per-wave 32 x 128 B output staging
+
+// s_waitcnt lgkmcnt(0), other counters untouched.
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+template <int RD>
+struct SCfg {
+  static constexpr int kFUnits = kSTok * RD * 4 / 1024;  // table rows: 32 x rd/2 x 8 B
+  static constexpr int kUnits = kSXUnits + kFUnits;
+  static constexpr int kUnitsW = kUnits / 4;             // copies per wave and tile
+  static constexpr int kSlotBytes = kUnits * 1024;
+  static constexpr int kLds = kSRing * kSlotBytes + kSStageBytes;
+  static_assert(kUnits % 4 == 0, "copy units split evenly over the 4 waves");
+};
+
+struct SProjParams {
+  const uint16_t* x;    // [M, 256] qr
+  const uint16_t* w;    // [N, 256]
+  uint16_t* q;          // [M, N]
+  const float* freqs;   // [S, rd/2, 2]
+  int32_t M, N, D, H, S;
+  int32_t ngroups;      // N / 256
+  int32_t nstreams;     // token runs; grid = ngroups * nstreams
+  int32_t ntiles;       // ceil(M / 32)
+  int32_t xcd_map;      // grid is a multiple of 8 * ngroups
+};
+
+// rope_pair with the mode fixed at compile time and torch-ROCm's unroll-slot
+// choice made by selects instead of a branch (the same operations and roundings).
+template <int RM>
+__device__ __forceinline__ void rope_pair_sel(float a, float b, float c, float d, uint32_t n, float& re,
+                                              float& im) {
+  if constexpr (RM == DSA_ROPE_CPU) {
+    re = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, d));
+    im = __fadd_rn(__fmul_rn(a, d), __fmul_rn(b, c));
+  } else {
+    const bool s3 = ((n >> 7) & 3u) == 3u;
+    const float ac = __fmul_rn(a, c), bd = __fmul_rn(b, d), ad = __fmul_rn(a, d), bc = __fmul_rn(b, c);
+    re = s3 ? __fmaf_rn(-b, d, ac) : __fmaf_rn(a, c, -bd);
+    im = s3 ? __fadd_rn(ad, bc) : __fmaf_rn(b, c, ad);
+  }
+}
+
+template <int RD, int RM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void ix_proj_k256_kernel(
+    SProjParams p) {
+  using C = SCfg<RD>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wi = tid >> 6;
+  const int wis = __builtin_amdgcn_readfirstlane(wi);
+  const int r32 = lane & 31, g = lane >> 5;
+
+  int cg, st;
+  {
+    const int i = blockIdx.x;
+    if (p.xcd_map) {
+      const int j = i >> 3;
+      cg = j % p.ngroups;
+      st = (j / p.ngroups) * 8 + (i & 7);
+    } else {
+      cg = i % p.ngroups;
+      st = i / p.ngroups;
+    }
+  }
+  const int t0 = (int)((int64_t)st * p.ntiles / p.nstreams);
+  const int t1 = (int)((int64_t)(st + 1) * p.ntiles / p.nstreams);
+  const int n0 = cg * kSCh;
+
+  const i32x4 xrs = make_rsrc(p.x, (uint32_t)p.M * (uint32_t)(kSK * 2));
+  const i32x4 frs = make_rsrc(p.freqs, RD > 0 ? (uint32_t)p.S * (uint32_t)(RD * 4) : 0u);
+  const __amdgpu_buffer_rsrc_t qrs = buf_rsrc(p.q, (uint32_t)p.M * (uint32_t)p.N * 2u);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+
+  // This wave's W: rows n0 + 64 wi + 32 i + r32, k chunk 2 ks + g (8 bf16).
+  // This wave's W in MFMA A-operand layout: wf[i][ks] of lane (r32, g) holds row
+  // n0 + 64 wi + 32 i + r32, k 16 ks + 8 g .. + 7. Loaded straight from global
+  // memory every instruction would touch 32 rows (32 cache lines); instead each
+  // wave copies its 32 rows of tile i (16 KB, contiguous in W) into LDS with 1 KB
+  // copies, position P holding row P/32, chunk (P%32) ^ (row%16), and reads the
+  // fragments from there (two passes through the first 64 KB of LDS).
+  bf16x8 wf[2][16];
+  {
+    static_assert(4 * 16 * 1024 <= C::kLds, "W staging fits the workgroup's LDS");
+    const i32x4 wrs = make_rsrc(p.w, (uint32_t)p.N * (uint32_t)(kSK * 2));
+    const uint32_t wbase = lds0 + (uint32_t)wis * 16384u;
+    const u32x4* wl = reinterpret_cast<const u32x4*>(smem + wi * 16384);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t rbase = (uint32_t)(n0 + 64 * wis + 32 * i) * (uint32_t)(kSK * 2);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int P = 64 * u + lane, row = P >> 5;
+        lds_dma16(wrs, rbase + (uint32_t)row * (uint32_t)(kSK * 2) + 16u * (uint32_t)((P & 31) ^ (row & 15)),
+                  wbase + 1024u * (uint32_t)u);
+      }
+      wait_vmcnt<0>();
+      __syncthreads();
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) wf[i][ks] = __builtin_bit_cast(bf16x8, wl[r32 * 32 + ((2 * ks + g) ^ (r32 & 15))]);
+      wait_lgkmcnt0();  // the reads are done before the region is copied over again
+      __syncthreads();
+    }
+  }
+
+  // Copy unit u of a slot covers 64 16-byte positions. qr region: position P holds
+  // row P/32, chunk (P%32) ^ (row%16) (16 lanes reading one k chunk of 16 rows hit
+  // 16 different bank groups; k-steps ks and ks + 8 are 256 bytes apart). Table region: position P holds row P/(RD/4),
+  // chunk (P%(RD/4)) ^ (row % (RD/4)) of that token's RD*4-byte table row. Each wave
+  // moves units wi, wi + 4, ...: with RD = 32 its last unit (16 + wi) is table rows.
+  constexpr int kXW = kSXUnits / 4;  // qr units per wave
+  int xrow[kXW];
+  uint32_t xoff[kXW];
+#pragma unroll
+  for (int i = 0; i < kXW; ++i) {
+    const int P = 64 * (wis + 4 * i) + lane;
+    xrow[i] = P >> 5;
+    xoff[i] = (uint32_t)xrow[i] * (uint32_t)(kSK * 2) + 16u * (uint32_t)((P & 31) ^ (xrow[i] & 15));
+  }
+  constexpr int kCpr = RD > 0 ? RD / 4 : 1;  // 16-byte chunks per table row
+  int frow = 0, fpos = 0;                    // table unit: tile row, and its position (m % S)
+  uint32_t fcol = 0;
+  if constexpr (RD > 0) {
+    static_assert(SCfg<RD>::kFUnits == 4, "one table unit per wave");
+    const int P = 64 * wis + lane;
+    frow = P / kCpr;
+    fcol = 16u * (uint32_t)((P % kCpr) ^ (frow % kCpr));
+    fpos = (int)((uint32_t)(t0 * kSTok + frow) % (uint32_t)p.S);
+  }
+  // Copies of tile t (tiles are issued in order t0, t0 + 1, ...; fpos follows).
+  auto issue = [&](int t, int slot) {
+    const uint32_t base = lds0 + (uint32_t)slot * C::kSlotBytes;
+    const int lim = p.M - t * kSTok;  // rows of the tile below M
+    const uint32_t mb = (uint32_t)(t * kSTok) * (uint32_t)(kSK * 2);
+#pragma unroll
+    for (int i = 0; i < kXW; ++i)
+      lds_dma16(xrs, xrow[i] < lim ? mb + xoff[i] : kOob, base + 1024u * (uint32_t)(wis + 4 * i));
+    if constexpr (RD > 0) {
+      lds_dma16(frs, frow < lim ? (uint32_t)fpos * (uint32_t)(RD * 4) + fcol : kOob,
+                base + 1024u * (uint32_t)(kSXUnits + wis));
+      fpos += kSTok;
+      if (fpos >= p.S) {
+        fpos -= p.S;
+        if (fpos >= p.S) fpos = (int)((uint32_t)fpos % (uint32_t)p.S);
+      }
+    }
+  };
+
+  if (t0 < t1) issue(t0, 0);
+  if (t0 + 1 < t1) issue(t0 + 1, 1);
+  uint8_t* wst = smem + kSRing * C::kSlotBytes + wi * (kSTok * 128);  // this wave's staging
+  const int D = p.D;
+  for (int t = t0; t < t1; ++t) {
+    const int it = t - t0;
+    // Operations issued after this tile's copies: the stores of tile t - 2 (when
+    // it >= 2; waiting for them too is harmless), the copies of tile t + 1 and the
+    // stores of tile t - 1.
+    if (t + 1 < t1) {
+      if (it >= 1) wait_vmcnt<C::kUnitsW + kSStoresW>();
+      else wait_vmcnt<C::kUnitsW>();
+    } else {
+      if (it >= 1) wait_vmcnt<kSStoresW>();
+      else wait_vmcnt<0>();
+    }
+    __syncthreads();  // tile t is in LDS; every wave is done with the slot of tile t - 1
+    if (t + 2 < t1) issue(t + 2, (it + 2) % kSRing);
+    const uint8_t* slot = smem + (it % kSRing) * C::kSlotBytes;
+    const u32x4* xs = reinterpret_cast<const u32x4*>(slot);
+
+    // B fragments are read kPre k-steps ahead of their products (one LDS read per
+    // two MFMAs in the issue order, pinned below; fewer with the RoPE epilogue's
+    // registers).
+    constexpr int kPre = RD > 0 ? 4 : 8;
+    f32x16 acc0 = f32x16{}, acc1 = f32x16{};
+    bf16x8 bq[16];
+#pragma unroll
+    for (int ks = 0; ks < kPre; ++ks) bq[ks] = __builtin_bit_cast(bf16x8, xs[r32 * 32 + ((2 * ks + g) ^ (r32 & 15))]);
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      if (ks + kPre < 16)
+        bq[ks + kPre] = __builtin_bit_cast(bf16x8, xs[r32 * 32 + ((2 * (ks + kPre) + g) ^ (r32 & 15))]);
+      acc0 = mfma32x32x16(wf[0][ks], bq[ks], acc0);
+      acc1 = mfma32x32x16(wf[1][ks], bq[ks], acc1);
+    }
+#pragma unroll
+    for (int ks = 0; ks < kPre; ++ks) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      if (ks + kPre < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                      // 2 MFMA
+    }
+
+    // Epilogue: lane (r32, g), register r of tile i is channel
+    // n0 + 64 wi + 32 i + 8 (r/4) + 4 g + r%4 of token m0 + r32.
+    const int m = t * kSTok + r32;
+    const uint8_t* fr = slot + kSXUnits * 1024;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const f32x16& a = i ? acc1 : acc0;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        uint32_t u0 = pack_bf2(a[4 * q4], a[4 * q4 + 1]);
+        uint32_t u1 = pack_bf2(a[4 * q4 + 2], a[4 * q4 + 3]);
+        if constexpr (RD > 0) {
+          const int c = n0 + 64 * wis + 32 * i + 8 * q4;  // + 4 g; the 8-group is rotated or not as a whole
+          const int d0 = c % D;
+          if (d0 >= D - RD) {
+            constexpr int kCpr = RD / 4;
+            const int pj = (d0 - (D - RD)) / 2 + 2 * g;  // complex index of (u0), (u1) is pj + 1
+            const float4 cs = *reinterpret_cast<const float4*>(fr + (r32 * kCpr + ((pj >> 1) ^ (r32 % kCpr))) * 16);
+            // Only (n / 128) % 4 of the flat complex index n matters: 32-bit wrap is exact.
+            const uint32_t nb = ((uint32_t)m * (uint32_t)p.H + (uint32_t)(c / D)) * (uint32_t)(RD / 2) + (uint32_t)pj;
+            float re, im;
+            rope_pair_sel<RM>(bf_lo(u0), bf_hi(u0), cs.x, cs.y, nb, re, im);
+            u0 = pack_bf2(re, im);
+            rope_pair_sel<RM>(bf_lo(u1), bf_hi(u1), cs.z, cs.w, nb + 1, re, im);
+            u1 = pack_bf2(re, im);
+          }
+        }
+        const int ck = 4 * i + q4;  // 16-byte chunk of the wave's 128-byte row piece
+        *reinterpret_cast<uint2*>(wst + r32 * 128 + ((ck ^ (r32 & 7)) * 16) + 8 * g) = uint2{u0, u1};
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < kSStoresW; ++k) {
+      const int row = 8 * k + (lane >> 3), ch = lane & 7;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(wst + row * 128 + ((ch ^ (row & 7)) * 16));
+      const uint32_t mm = (uint32_t)(t * kSTok + row);
+      // Rows at or past M are beyond the resource and dropped.
+      const uint32_t off = mm < (uint32_t)p.M ? (mm * (uint32_t)p.N + (uint32_t)(n0 + 64 * wis + 8 * ch)) * 2u
+                                              : 0xfffffff0u;
+      __builtin_amdgcn_raw_buffer_store_b128(v, qrs, (int)off, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+template <int RD, int RM>
+int launch_k256(const ProjParams& a, void* stream) {
+  using C = SCfg<RD>;
+  int cus = 0;
+  if (dsa_host::device_cu_count(&cus) != DSA_OK) return DSA_ERR_DEVICE;
+  SProjParams p;
+  p.x = a.x;
+  p.w = a.w;
+  p.q = a.q;
+  p.freqs = a.freqs;
+  p.M = (int32_t)a.M;
+  p.N = a.N;
+  p.D = a.D;
+  p.H = a.H;
+  p.S = a.S;
+  p.ngroups = a.N / kSCh;
+  p.ntiles = (int32_t)((a.M + kSTok - 1) / kSTok);
+  // Two workgroups per CU; the token runs of one XCD's workgroups share qr tiles.
+  int streams = (2 * cus) / p.ngroups;
+  if (streams < 1) streams = 1;
+  if (streams >= 8) streams -= streams % 8;
+  if (streams > p.ntiles) streams = p.ntiles;
+  p.nstreams = streams;
+  p.xcd_map = streams % 8 == 0 ? 1 : 0;
+  const int64_t blocks = (int64_t)streams * p.ngroups;
+  void (*fn)(SProjParams) = ix_proj_k256_kernel<RD, RM>;
+  if (dsa_host::ensure_dyn_lds((const void*)fn, C::kLds) != DSA_OK) return DSA_ERR_LAUNCH;
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), (size_t)C::kLds,
+                     (hipStream_t)stream, p);
+  return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
 }  // namespace
 
 extern "C" int dsa_indexer_q_proj(const void* qr, const void* wq, const void* freqs_cis,
@@ -222,6 +518,13 @@ extern "C" int dsa_indexer_q_proj(const void* qr, const void* wq, const void* fr
   p.rd = (int32_t)rd;
   p.S = (int32_t)s_len;
   p.rope_mode = rope_mode;
+  // k = 256 with a table of at most 32 rotated channels per head: W-stationary kernel.
+  if (k == kSK && m <= INT32_MAX / 2 && m * n <= (int64_t)UINT32_MAX / 2) {
+    if (freqs_cis == nullptr) return launch_k256<0, 0>(p, stream);
+    if (rd == 32)
+      return rope_mode == DSA_ROPE_CPU ? launch_k256<32, DSA_ROPE_CPU>(p, stream)
+                                       : launch_k256<32, DSA_ROPE_TORCH_ROCM>(p, stream);
+  }
   const int64_t blocks = (m + kTM - 1) / kTM * (n / kTN);
   if (blocks > INT32_MAX) return DSA_ERR_SHAPE;
   const size_t smem = (size_t)kStages * kStageBytes;

@@ -138,12 +138,35 @@ class Model(nn.Module):
         k_out = min(self.index_topk, n_cand)
         if k_out <= 0:
             return torch.empty(bsz, seqlen, 0, dtype=torch.int64, device=x.device)
-        q = self.wq_b(qr).unflatten(-1, (self.n_local_heads, self.head_dim))
+        freqs = self.freqs_cis[start_pos:end_pos]
+        if self._q_proj_fused(qr):
+            # q = RoPE(qr . wq_b^T) in one kernel, bit-equal to F.linear + apply_rotary_emb
+            # (task2_v0_ref.py:129-131) for this shape class.
+            q = _native.indexer_q_proj(qr, self.wq_b.weight, freqs, self.head_dim, self.rope_head_dim,
+                                       self.rope_mode)
+            freqs = None
+        else:
+            q = self.wq_b(qr).unflatten(-1, (self.n_local_heads, self.head_dim))
         wl = self.weights_proj(x)
         w_scale = self.softmax_scale * self.n_heads ** -0.5
         return _native.indexer_score_topk(
-            q, self.kv_cache, wl, w_scale, self.freqs_cis[start_pos:end_pos], self.rope_head_dim,
+            q, self.kv_cache, wl, w_scale, freqs, self.rope_head_dim,
             n_cand, k_out, ratio, start_pos == 0, offset, self.rope_mode)
+
+    #: smallest token count (b * s) for which the fused query projection is used
+    Q_PROJ_MIN_TOKENS = 64
+
+    def _q_proj_fused(self, qr: torch.Tensor) -> bool:
+        """Whether q comes from dsa_indexer_q_proj instead of F.linear + RoPE in the score
+        kernel: q_lora_rank 256, rope_head_dim 32, bf16, at least 64 tokens. There the
+        kernel's natural-order k accumulation equals torch-ROCm's F.linear bit for bit
+        (tests/test_gpu_indexer_proj.py sweeps the token count); below 64 tokens hipBLASLt
+        switches to algorithms that reduce k in another order, so F.linear stays."""
+        w = self.wq_b.weight
+        return (qr.is_cuda and qr.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+                and qr.shape[-1] == 256 and self.rope_head_dim == 32
+                and w.shape[0] % 256 == 0 and self.head_dim in (64, 128)
+                and qr.shape[0] * qr.shape[1] >= self.Q_PROJ_MIN_TOKENS)
 
 
 ModelNew = Model

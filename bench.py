@@ -10,9 +10,10 @@ Also reported, each with hot-cache times and times with the 256 MB MALL flushed
 (512 MB written before every call):
   task1_c1      configs[0] on the GPU, beside the reference path on the host CPU;
   task1_c4      the true-gather kernel at configs[3] (MFMA-bound);
-  task2         configs[2]: Model.forward (two torch projections + the fused score /
-                top-k kernel) and the fused kernel alone, with its HBM and MFMA
-                rooflines and the reference path on the host CPU;
+  task2         configs[2]: Model.forward (query projection + RoPE kernel, the
+                weights projection in torch, the fused score / top-k kernel), the
+                fused kernel and the projection kernel alone with their rooflines,
+                and the reference path on the host CPU;
   dsa_layer_c5  configs[4]: the wide indexer, sparse MLA, and the whole prefill layer
                 (indexer Model.forward whose int64 top-2048 feeds sparse MLA);
   dsa_decode_c5 one configs[4] decode step, HIP-graph replayed and eager.
@@ -49,9 +50,10 @@ def t2_bytes(b=8, s=2600, dim=1024, ql=256, t=650, d=64, h=16, rd=32, k=128):
             + s * (rd // 2) * 8 + b * s * k * 8)
 
 
-def t2_kernel_bytes(b=8, s=2600, t=650, d=64, h=16, rd=32, k=128):
-    """The fused kernel: q read (pre-RoPE), wl read, kv_cache, freqs rows, int64 output."""
-    return b * s * h * d * 2 + b * s * h * 2 + b * t * d * 2 + s * (rd // 2) * 8 + b * s * k * 8
+def t2_kernel_bytes(b=8, s=2600, t=650, d=64, h=16, k=128):
+    """The fused kernel as Model.forward runs it: q read (already rotated by the projection
+    kernel), wl read, kv_cache, int64 output."""
+    return b * s * h * d * 2 + b * s * h * 2 + b * t * d * 2 + b * s * k * 8
 
 
 def _events_time(torch, fn, steps, stream):
@@ -403,15 +405,28 @@ def main():
             _warm(torch, lambda: m2(x, qr, sp, off), a.warmup, 0.2)
             ms2 = _events_time(torch, lambda: m2(x, qr, sp, off), a.steps, stream)
             m2_cold = cold(lambda: m2(x, qr, sp, off), 10)
-            qp = torch.nn.functional.linear(qr, m2.wq_b.weight).unflatten(-1, (16, 64)).contiguous()
-            wl = torch.nn.functional.linear(x, m2.weights_proj.weight)
+            # The kernels as Model.forward runs them: q projected and rotated by
+            # dsa_indexer_q_proj, wl by F.linear, then the fused score / top-k kernel.
             fr = m2.freqs_cis[:2600]
+            assert m2._q_proj_fused(qr)
+            pfn = lambda: _native.indexer_q_proj(qr, m2.wq_b.weight, fr, 64, 32)
+            qp = pfn()
+            wl = torch.nn.functional.linear(x, m2.weights_proj.weight)
             scale = 64 ** -0.5 * 16 ** -0.5
-            kfn = lambda: _native.indexer_score_topk(qp, m2.kv_cache, wl, scale, fr, 32, 650, 128, 4, True, 0)
+            kfn = lambda: _native.indexer_score_topk(qp, m2.kv_cache, wl, scale, None, 32, 650, 128, 4, True, 0)
             _warm(torch, kfn, 3, 0.1)
             msk = _events_time(torch, kfn, a.steps, stream)
             k_cold = cold(kfn, 10)
+            _warm(torch, pfn, 3, 0.1)
+            msp = _events_time(torch, pfn, a.steps, stream)
+            # torch's projection for comparison (F.linear; RoPE then runs inside the score kernel)
+            lfn = lambda: torch.nn.functional.linear(qr, m2.wq_b.weight)
+            _warm(torch, lfn, 3, 0.1)
+            msl = _events_time(torch, lfn, a.steps, stream)
         kb = t2_kernel_bytes()
+        proj_flop = 2 * 8 * 2600 * 1024 * 256
+        # qr read, wq_b read, q written, the RoPE table rows read
+        proj_bytes = 8 * 2600 * 256 * 2 + 1024 * 256 * 2 + 8 * 2600 * 1024 * 2 + 2600 * 16 * 8
         score_flop = 2 * 16 * 64 * sum(((t + 1) // 4) for t in range(2600)) * 8
         result["task2"] = {
             "workload": "task2_indexer configs[2]: x[8,2600,1024], qr[8,2600,256], kv_cache[8,650,64], "
@@ -429,6 +444,16 @@ def main():
             # fractions are reported, the HBM one as "roofline".
             "roofline": _roofline_hbm(kb, msk, _traffic("ix_score_topk_kernel")),
             "roofline_mfma": _roofline_mfma(score_flop, msk),
+            "q_proj": {
+                "kernel": "ix_proj_k256_kernel (q = RoPE(qr . wq_b^T), bit-equal to F.linear + apply_rotary_emb)",
+                "us": round(msp * 1e3, 2),
+                "flop": proj_flop,
+                "TFLOPs": round(proj_flop / (msp * 1e-3) / 1e12, 1),
+                "bytes": proj_bytes,
+                "GBps": round(proj_bytes / (msp * 1e-3) / 1e9, 1),
+                "roofline_mfma": _roofline_mfma(proj_flop, msp),
+                "torch_f_linear_us": round(msl * 1e3, 2),
+            },
         }
         t2_cpu_inputs = (m2.wq_b.weight.detach().cpu(), m2.weights_proj.weight.detach().cpu(),
                          init[2].cpu(), x.cpu(), qr.cpu())

@@ -13,8 +13,10 @@ import numpy as np
 import pytest
 import torch
 
+from conftest import bits_of
 from ascendc_kernel_amd import _native
 from oracle import indexer as oix
+from oracle import rules
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +37,11 @@ def _case(k, n, d, rd, b, m, seed, dev):
 
 
 SHAPES = {"c3": (256, 1024, 64, 32), "c5": (1536, 8192, 128, 64)}
-EQUAL = [("c3", 8, 2600), ("c3", 1, 8), ("c3", 1, 64), ("c3", 1, 129), ("c3", 2, 1000), ("c3", 1, 5000),
+# The configs[2] class (k = 256) is what Model.forward routes through the kernel from 64
+# tokens up (task2_indexer.Model._q_proj_fused), so its token counts are swept densely.
+EQUAL = [("c3", 8, 2600), ("c3", 1, 8), ("c3", 1, 64), ("c3", 1, 65), ("c3", 1, 96), ("c3", 3, 100),
+         ("c3", 1, 129), ("c3", 1, 255), ("c3", 1, 640), ("c3", 2, 1000), ("c3", 1, 2048), ("c3", 4, 2600),
+         ("c3", 1, 5000), ("c3", 3, 7777), ("c3", 1, 8192), ("c3", 8, 4096), ("c3", 16, 2600),
          ("c5", 1, 8192), ("c5", 1, 64), ("c5", 1, 1000), ("c5", 1, 4096), ("c5", 2, 200)]
 
 
@@ -70,3 +76,17 @@ def test_q_proj_small_token_counts(gpu, shape):
         bad = (a - r).abs() > ulp + 2 * k * 2.0 ** -24 * mag
         assert not bool(bad.any()), (m, int(bad.sum()))
     _say(f"[q_proj {shape}] outputs differing from F.linear for m = 1..16:", counts)
+
+
+@pytest.mark.parametrize("b,m", [(1, 64), (2, 1000), (8, 2600)])
+def test_q_proj_cpu_rope_rounding(gpu, b, m):
+    """rope_mode DSA_ROPE_CPU (the CPU reference's non-FMA complex product): F.linear's q
+    rotated by the oracle's CPU rule (oracle/rules.py rope 'cpu', pinned by the reference
+    fixture) equals the kernel's output."""
+    k, n, d, rd = SHAPES["c3"]
+    w, qr, fr, ref, _ = _case(k, n, d, rd, b, m, 300 + m, gpu)
+    got = _native.indexer_q_proj(qr, w, fr, d, rd, _native.DSA_ROPE_CPU)
+    f = torch.view_as_real(fr).reshape(m, rd // 2, 2).cpu().numpy()
+    want = rules.rope_bf16(bits_of(ref), f, rd, "cpu")
+    ne = int((bits_of(got) != want).sum())
+    assert ne == 0, f"{ne} of {want.size} outputs differ"

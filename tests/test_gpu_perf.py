@@ -58,7 +58,8 @@ def _settled_us(fn, reps, min_seconds=0.3):
 
 # Kernel-time budgets in microseconds (hot caches, settled clock): a regression of the
 # kernels past these fails. Measured values are printed.
-BUDGET_US = {"c2": 125.0, "c3_kernel": 65.0, "c4": 420.0, "c5_mla": 5500.0}
+BUDGET_US = {"c2": 125.0, "c3_kernel": 60.0, "c3_q_proj": 24.0, "c3_model": 85.0, "c4": 420.0,
+             "c5_mla": 5500.0}
 
 
 def test_budget_task1_c2(gpu):
@@ -83,6 +84,22 @@ def test_budget_task2_c3_kernel(gpu):
         us = _settled_us(fn, 50)
     print(f"[budget c3 fused kernel] {us:.1f} us (budget {BUDGET_US['c3_kernel']})", flush=True)
     assert us <= BUDGET_US["c3_kernel"]
+
+
+def test_budget_task2_c3_q_proj_and_model(gpu):
+    """The query projection + RoPE kernel and the whole Model.forward at configs[2]."""
+    from ascendc_kernel_amd import _native
+    torch.manual_seed(42)
+    m = t2.Model(*t2.get_init_inputs(device=gpu)).to(gpu)
+    x, qr, sp, off = t2.get_inputs(device=gpu)
+    assert m._q_proj_fused(qr)
+    with torch.no_grad():
+        us_p = _settled_us(lambda: _native.indexer_q_proj(qr, m.wq_b.weight, m.freqs_cis[:2600], 64, 32), 50)
+        us_m = _settled_us(lambda: m(x, qr, sp, off), 50)
+    print(f"[budget c3 q_proj] {us_p:.1f} us (budget {BUDGET_US['c3_q_proj']}); "
+          f"[budget c3 Model.forward] {us_m:.1f} us (budget {BUDGET_US['c3_model']})", flush=True)
+    assert us_p <= BUDGET_US["c3_q_proj"]
+    assert us_m <= BUDGET_US["c3_model"]
 
 
 def test_budget_task1_c4(gpu):
