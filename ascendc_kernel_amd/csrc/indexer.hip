@@ -90,6 +90,9 @@ __device__ __forceinline__ int n_valid(const IxParams& p, int t) {
   return n < p.T ? n : p.T;
 }
 
+// bf16(x) (round to nearest even) as an fp32 value, one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ float bf16_as_f32(float x) { return __builtin_bit_cast(float, pack_bf2(0.f, x)); }
+
 __device__ __forceinline__ void lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
 // Per half-wave: the bin b of a 256-bin histogram (bins ascending in key) with
@@ -277,15 +280,16 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
       pk[k] = (uint32_t)sw[0];
       pk[k + 4] = (uint32_t)sw[1];
     }
-    // * w -> bf16 (the products are exact in fp32), as fp32 values.
+    // * w -> bf16 (the products are exact in fp32), as fp32 values: one
+    // v_cvt_pk_bf16_f32 with a zero low operand leaves bf16(x) in the high half and
+    // zeros below it, which is bf16(x) as an fp32 value.
     float v[16];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int r = 2 * k;
       const int h0 = (r < 4) ? r : (r < 8) ? r + 4 : (r < 12) ? r - 4 : r;
-      const uint32_t pb = pack_bf2(bf_lo(pk[k]) * w[h0], bf_hi(pk[k]) * w[h0 + 1]);
-      v[r] = bf_lo(pb);
-      v[r + 1] = bf_hi(pb);
+      v[r] = bf16_as_f32(bf_lo(pk[k]) * w[h0]);
+      v[r + 1] = bf16_as_f32(bf_hi(pk[k]) * w[h0 + 1]);
     }
     // Head j is in slot j (j<4), j+4 -> slot j+8, j+8 -> slot j+4, j+12 -> slot j+12;
     // IEEE fp32 adds in torch's order. torch's four accumulators start at +0; adding
@@ -341,10 +345,17 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   *reinterpret_cast<u32x4*>(myhist + 8 * hl) = u32x4{0u, 0u, 0u, 0u};
   *reinterpret_cast<u32x4*>(myhist + 8 * hl + 4) = u32x4{0u, 0u, 0u, 0u};
   lds_fence();
-  for (int tile = 0; tile < ntile; ++tile) {
-    const int c = 32 * tile + hl;
-    const uint16_t u = keys[(half * ntile_all + tile) * 32 + hl];
-    if (c < nv && (int)(u >> 8) == b1) atomicAdd(&myhist[u & 255u], 1u);
+  // Four tiles' keys are read before their atomics so the LDS reads overlap (reads
+  // past the last tile stay inside the workgroup's LDS and are not used).
+  for (int tile0 = 0; tile0 < ntile; tile0 += 4) {
+    uint32_t u4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) u4[j] = keys[(half * ntile_all + tile0 + j) * 32 + hl];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = 32 * (tile0 + j) + hl;
+      if (c < nv && (int)(u4[j] >> 8) == b1) atomicAdd(&myhist[u4[j] & 255u], 1u);
+    }
   }
   if (hl == 0 && nmask > 0 && b1 == (int)(kNegInfKey >> 8)) atomicAdd(&myhist[kNegInfKey & 255u], nmask);
   lds_fence();
@@ -367,25 +378,33 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   };
   const uint32_t ltmask = (1u << hl) - 1u;
   uint32_t gt_run = 0, eq_run = 0;
-  for (int tile = 0; tile < ntile; ++tile) {
-    const int c = 32 * tile + hl;
-    const uint32_t u = keys[(half * ntile_all + tile) * 32 + hl];
-    const bool valid = c < nv;
-    const bool gt = valid && u > V;
-    const bool eq = valid && u == V;
-    const uint32_t gm = (uint32_t)(__ballot(gt) >> (32 * half));
-    const uint32_t em = (uint32_t)(__ballot(eq) >> (32 * half));
-    if (gt) {
-      const uint32_t pos = gt_run + __builtin_popcount(gm & ltmask);
-      if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
+  for (int tile0 = 0; tile0 < ntile; tile0 += 4) {
+    uint32_t u4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) u4[j] = keys[(half * ntile_all + tile0 + j) * 32 + hl];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tile = tile0 + j;
+      if (tile >= ntile) break;
+      const int c = 32 * tile + hl;
+      const uint32_t u = u4[j];
+      const bool valid = c < nv;
+      const bool gt = valid && u > V;
+      const bool eq = valid && u == V;
+      const uint32_t gm = (uint32_t)(__ballot(gt) >> (32 * half));
+      const uint32_t em = (uint32_t)(__ballot(eq) >> (32 * half));
+      if (gt) {
+        const uint32_t pos = gt_run + __builtin_popcount(gm & ltmask);
+        if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
+      }
+      const uint32_t er = eq_run + __builtin_popcount(em & ltmask);
+      if (eq && er < need_eq) {
+        const uint32_t pos = n_gt + er;
+        if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
+      }
+      gt_run += __builtin_popcount(gm);
+      eq_run += __builtin_popcount(em);
     }
-    const uint32_t er = eq_run + __builtin_popcount(em & ltmask);
-    if (eq && er < need_eq) {
-      const uint32_t pos = n_gt + er;
-      if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
-    }
-    gt_run += __builtin_popcount(gm);
-    eq_run += __builtin_popcount(em);
   }
   const uint32_t eq_taken = eq_run < need_eq ? eq_run : need_eq;
   if (V == kNegInfKey) {

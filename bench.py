@@ -56,6 +56,11 @@ def t2_kernel_bytes(b=8, s=2600, t=650, d=64, h=16, k=128):
     return b * s * h * d * 2 + b * s * h * 2 + b * t * d * 2 + b * s * k * 8
 
 
+def _say(msg):
+    """Progress line on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def _events_time(torch, fn, steps, stream):
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -227,6 +232,7 @@ def main():
     }
     del q, kv, idx
 
+    _say("configs[1] headline done")
     # ---------------- Task1 configs[0] (the reference's CPU config) on the GPU
     # (the reference's get_inputs draws with batch_size 1 and seq_len 160, seed 42)
     torch.manual_seed(42)
@@ -244,6 +250,7 @@ def main():
         "algorithmic_bytes": t1_bytes(1, 160, 64, 128, 32, 16)}
     del q1, kv1, idx1
 
+    _say("configs[0] done")
     # ---------------- Task1 true-gather
     if not a.no_c4:
         torch.cuda.empty_cache()
@@ -272,6 +279,7 @@ def main():
         }
         del q4, kv4, idx4
 
+    _say("configs[3] done")
     # ---------------- Decode at the configs[4] size (before the prefill legs, so that the
     # prefill calls stay the last dispatches of their kernels): one DSA step for one new
     # token at position 8191 (indexer Model.forward, then sparse MLA over its int64
@@ -319,6 +327,7 @@ def main():
         del graph, outd, xd, qrd, qd, kvd, ixd, mlad
         torch.cuda.empty_cache()
 
+    _say("configs[4] decode done")
     # ---------------- DSA layer: wide indexer + sparse MLA, and the layer
     # chained as in the reference (task2_v0_ref.py:138-143 output -> task1_v0_ref.py:8-12).
     if not a.no_c5:
@@ -390,6 +399,7 @@ def main():
         del qm, kvm, idxm, picks, x5, qr5, ix5, mla
         torch.cuda.empty_cache()
 
+    _say("configs[4] prefill done")
     # ---------------- Task2
     t2_cpu_inputs = None
     if not a.no_task2:
@@ -462,6 +472,7 @@ def main():
     if not a.no_decode:
         result["dsa_decode_c5"] = dsa_decode
 
+    _say("configs[2] done")
     # ---------------- The reference path on the host CPU cores (the oracle's restatement
     # of the reference modules), on the same seeded inputs, after every GPU leg.
     if not a.no_cpu:
