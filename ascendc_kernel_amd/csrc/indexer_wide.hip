@@ -195,15 +195,19 @@ __device__ void radix_pass_desc(const uint32_t* src, uint32_t* dst, int n, int s
   }
   __syncthreads();
   // Exclusive scan of the digit totals (digit order = output order), then the
-  // start of every (wave, digit) block, written over the counts.
-  constexpr int kQ = 256 / (64 * NW);  // digits per thread
+  // start of every (wave, digit) block, written over the counts. Threads
+  // 0 .. 64 kSW - 1 take kQ digits each (with more than 256 threads, the first 256
+  // take one and the others only meet the barriers).
+  constexpr int kQ = (256 / (64 * NW)) > 0 ? 256 / (64 * NW) : 1;  // digits per scan thread
+  constexpr int kSW = 256 / (64 * kQ);                            // waves that scan
+  const bool scans = wv < kSW;
   uint32_t cnt[kQ][NW];
   uint32_t loc = 0u;
 #pragma unroll
   for (int i = 0; i < kQ; ++i)
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      cnt[i][w] = wr[w * 256 + kQ * tt + i];
+      cnt[i][w] = scans ? wr[w * 256 + kQ * tt + i] : 0u;
       loc += cnt[i][w];
     }
   uint32_t incl = loc;
@@ -212,17 +216,19 @@ __device__ void radix_pass_desc(const uint32_t* src, uint32_t* dst, int n, int s
     const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
     if (lane >= off) incl += o;
   }
-  if (lane == 63) wt[wv] = incl;
+  if (lane == 63 && scans) wt[wv] = incl;
   __syncthreads();
-  uint32_t run = incl - loc;
-  for (int w = 0; w < wv; ++w) run += wt[w];
+  if (scans) {
+    uint32_t run = incl - loc;
+    for (int w = 0; w < wv; ++w) run += wt[w];
 #pragma unroll
-  for (int i = 0; i < kQ; ++i)
+    for (int i = 0; i < kQ; ++i)
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      wr[w * 256 + kQ * tt + i] = run;
-      run += cnt[i][w];
-    }
+      for (int w = 0; w < NW; ++w) {
+        wr[w * 256 + kQ * tt + i] = run;
+        run += cnt[i][w];
+      }
+  }
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
@@ -589,11 +595,21 @@ struct SelParams {
   int64_t offset;
 };
 
-__global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
+// NT threads per workgroup: 256 (32 keys per thread) for many rows, 1024 (8 keys per
+// thread) when there are too few rows to fill the CUs (decode), where the row's
+// latency is the step's.
+template <int NT>
+constexpr int sel_hist_words() { return (NT / 64) * 256 > 1024 ? (NT / 64) * 256 : 1024; }
+
+template <int NT>
+__global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
+  constexpr int NW = NT / 64;
+  constexpr int KPT = kMaxT / NT;  // keys per thread
+  constexpr int KW = KPT / 4;      // 8-byte words per thread
   extern __shared__ __align__(16) uint8_t smem[];
-  uint32_t* hist = reinterpret_cast<uint32_t*>(smem);     // [1024]: h1 | h2, then radix counts
-  uint32_t* wt = hist + 1024;                              // [4] wave totals
-  int32_t* sel = reinterpret_cast<int32_t*>(wt + 4);      // [4]
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem);     // h1 | h2, then the radix counts
+  uint32_t* wt = hist + sel_hist_words<NT>();              // [NW] wave totals
+  int32_t* sel = reinterpret_cast<int32_t*>(wt + NW);     // [4]
   uint32_t* sortbuf = reinterpret_cast<uint32_t*>(sel + 4);  // [psort]
   uint32_t* tmpbuf = sortbuf + p.psort;                    // [psort]
   const int tt = threadIdx.x;
@@ -608,12 +624,12 @@ __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
   const int K = p.K;
   const bool selecting = nv > K;
   // Keys of this thread (8-byte loads: rows start 8-byte aligned, kstride % 4 == 0).
-  const uint2* src = reinterpret_cast<const uint2*>(p.keys + row * p.kstride) + 8 * tt;
-  const int c0 = 32 * tt;
+  const uint2* src = reinterpret_cast<const uint2*>(p.keys + row * p.kstride) + KW * tt;
+  const int c0 = KPT * tt;
   // Order keys are >= 0x007f (-inf), so 0 marks the positions past nv.
-  uint2 kw[8];
+  uint2 kw[KW];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < KW; ++i) {
     const int rem = nv - (c0 + 4 * i);  // valid keys in this piece
     kw[i] = rem > 0 ? src[i] : uint2{0u, 0u};
     if (rem == 1) kw[i] = uint2{kw[i].x & 0xffffu, 0u};
@@ -624,12 +640,12 @@ __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
     const uint32_t w = (e & 2) ? kw[e >> 2].y : kw[e >> 2].x;
     return (e & 1) ? (w >> 16) : (w & 0xffffu);
   };
-  for (int i = tt; i < 512; i += 256) hist[i] = 0u;
+  for (int i = tt; i < 512; i += NT) hist[i] = 0u;
   __syncthreads();
   uint32_t kth = 0u, n_gt = (uint32_t)nv, need_eq = 0u;
   if (selecting) {
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
+    for (int e = 0; e < KPT; ++e) {
       const uint32_t u = key_of(e);
       if (u != 0u) atomicAdd(&hist[u >> 8], 1u);
     }
@@ -645,7 +661,7 @@ __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
     __syncthreads();
     const uint32_t b1 = (uint32_t)sel[0];
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
+    for (int e = 0; e < KPT; ++e) {
       const uint32_t u = key_of(e);
       if (u != 0u && (u >> 8) == b1) atomicAdd(&hist[256 + (u & 255u)], 1u);
     }
@@ -671,7 +687,7 @@ __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
   const uint32_t kth_e = selecting ? kth : 0xffffffffu;
   uint32_t cnt = 0u;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) {
+  for (int e = 0; e < KPT; ++e) {
     const uint32_t u = key_of(e);
     cnt += (u > kth ? 1u : 0u) + (u == kth_e ? 0x10000u : 0u);
   }
@@ -687,7 +703,7 @@ __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
   for (int w = 0; w < wv; ++w) base += wt[w];
   uint32_t og = base & 0xffffu, oe = base >> 16;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) {
+  for (int e = 0; e < KPT; ++e) {
     const uint32_t u = key_of(e);
     const uint32_t comp = (u << 16) | (0xffffu - (uint32_t)(c0 + e));
     if (u > kth) {
@@ -699,10 +715,10 @@ __global__ __launch_bounds__(256) void ix_select_kernel(SelParams p) {
   }
   const int count = selecting ? K : nv;
   __syncthreads();
-  radix_pass_desc<4>(sortbuf, tmpbuf, count, 16, hist, wt, tt);
-  radix_pass_desc<4>(tmpbuf, sortbuf, count, 24, hist, wt, tt);
+  radix_pass_desc<NW>(sortbuf, tmpbuf, count, 16, hist, wt, tt);
+  radix_pass_desc<NW>(tmpbuf, sortbuf, count, 24, hist, wt, tt);
   int64_t* out_row = p.out + row * K;
-  for (int j = tt; j < K; j += 256) {
+  for (int j = tt; j < K; j += NT) {
     const uint32_t comp = sortbuf[j];
     out_row[j] = (j < count) ? (int64_t)(0xffffu - (comp & 0xffffu)) + p.offset : (int64_t)-1;
   }
@@ -834,10 +850,16 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
     sp.causal = p.causal;
     sp.psort = p.psort;
     sp.offset = offset;
-    const size_t smem2 = 1024 * 4 + 16 + 16 + (size_t)ps * 8;
-    if (dsa_host::ensure_dyn_lds((const void*)ix_select_kernel, (int)smem2) != DSA_OK)
-      return DSA_ERR_LAUNCH;
-    hipLaunchKernelGGL(ix_select_kernel, dim3((unsigned)(b * s)), dim3(256), smem2, stream, sp);
+    // Fewer rows than CUs (decode): 1024 threads per row; otherwise 256.
+    int cu = 0;
+    if (dsa_host::device_cu_count(&cu) != DSA_OK) return DSA_ERR_DEVICE;
+    const bool wide_rows = b * s < (int64_t)cu;
+    void (*sfn)(SelParams) = wide_rows ? ix_select_kernel<1024> : ix_select_kernel<256>;
+    const int snt = wide_rows ? 1024 : 256;
+    const size_t smem2 = (size_t)(wide_rows ? sel_hist_words<1024>() : sel_hist_words<256>()) * 4 +
+                         (size_t)(snt / 64) * 4 + 16 + (size_t)ps * 8;
+    if (dsa_host::ensure_dyn_lds((const void*)sfn, (int)smem2) != DSA_OK) return DSA_ERR_LAUNCH;
+    hipLaunchKernelGGL(sfn, dim3((unsigned)(b * s)), dim3(snt), smem2, stream, sp);
     if (hipGetLastError() != hipSuccess) return DSA_ERR_LAUNCH;
   }
   return DSA_OK;
