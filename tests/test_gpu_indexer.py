@@ -169,6 +169,11 @@ SMALL = [
     # 2600-token context (no mask, +offset), and a 40-token chunk before it
     (8, 1, 2599, 5, 128, 650),
     (8, 40, 2560, 0, 128, 650),
+    # either side of the fused query projection's 64-token gate, and 65 tokens of
+    # 13-token sequences (the projection's 32-token tiles span several batches)
+    (1, 63, 1500, 2, 128, 650),
+    (1, 64, 1500, 2, 128, 650),
+    (5, 13, 100, 0, 32, 650),
 ]
 
 
