@@ -90,6 +90,24 @@ __device__ __forceinline__ int n_valid(const IxParams& p, int t) {
   return n < p.T ? n : p.T;
 }
 
+// The middle of three unsigned values: med3(x, y, ~0) = max(x, y), med3(x, y, 0) =
+// min(x, y). The compiler turns this form into one v_med3_u32 (and, being its own
+// instruction, keeps the wait states a following DPP read of the result needs).
+__device__ __forceinline__ uint32_t med3_u32(uint32_t x, uint32_t y, uint32_t z) {
+  return max(min(x, y), min(max(x, y), z));
+}
+
+// v from lane (lane ^ m) within each 32-lane half (m in 1, 2, 4, 8, 16): DPP quad
+// permutations for 1 and 2, a row rotation by 8 for 8, ds_swizzle otherwise.
+__device__ __forceinline__ uint32_t xor_lanes(uint32_t v, int m) {
+  const int x = (int)v;
+  if (m == 1) return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+  if (m == 2) return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+  if (m == 8) return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false); // row_ror:8
+  if (m == 4) return (uint32_t)__builtin_amdgcn_ds_swizzle(x, (4 << 10) | 0x1F);
+  return (uint32_t)__builtin_amdgcn_ds_swizzle(x, (16 << 10) | 0x1F);
+}
+
 // bf16(x) (round to nearest even) as an fp32 value, one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ float bf16_as_f32(float x) { return __builtin_bit_cast(float, pack_bf2(0.f, x)); }
 
@@ -376,7 +394,6 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
     }
     return (u << 16) | (0xffffu - c);
   };
-  const uint32_t ltmask = (1u << hl) - 1u;
   uint32_t gt_run = 0, eq_run = 0;
   for (int tile0 = 0; tile0 < ntile; tile0 += 4) {
     uint32_t u4[4];
@@ -391,19 +408,30 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
       const bool valid = c < nv;
       const bool gt = valid && u > V;
       const bool eq = valid && u == V;
-      const uint32_t gm = (uint32_t)(__ballot(gt) >> (32 * half));
-      const uint32_t em = (uint32_t)(__ballot(eq) >> (32 * half));
+      // Ranks within the half from the 64-bit ballot: mbcnt counts the set lanes
+      // below this one; the upper half then drops the lower half's count.
+      const uint64_t gb = __builtin_amdgcn_ballot_w64(gt);
+      const uint32_t glo = (uint32_t)gb, ghi = (uint32_t)(gb >> 32);
+      const uint32_t g_lo_cnt = (uint32_t)__builtin_popcount(glo);
+      const uint32_t g_below = __builtin_amdgcn_mbcnt_hi(ghi, __builtin_amdgcn_mbcnt_lo(glo, 0u)) -
+                               (half ? g_lo_cnt : 0u);
       if (gt) {
-        const uint32_t pos = gt_run + __builtin_popcount(gm & ltmask);
+        const uint32_t pos = gt_run + g_below;
         if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
       }
-      const uint32_t er = eq_run + __builtin_popcount(em & ltmask);
-      if (eq && er < need_eq) {
-        const uint32_t pos = n_gt + er;
-        if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
+      gt_run += half ? (uint32_t)__builtin_popcount(ghi) : g_lo_cnt;
+      const uint64_t eb = __builtin_amdgcn_ballot_w64(eq);
+      if (eb != 0) {  // ties with the k-th key are rare: skip the tile otherwise
+        const uint32_t elo = (uint32_t)eb, ehi = (uint32_t)(eb >> 32);
+        const uint32_t e_lo_cnt = (uint32_t)__builtin_popcount(elo);
+        const uint32_t er = eq_run + __builtin_amdgcn_mbcnt_hi(ehi, __builtin_amdgcn_mbcnt_lo(elo, 0u)) -
+                            (half ? e_lo_cnt : 0u);
+        if (eq && er < need_eq) {
+          const uint32_t pos = n_gt + er;
+          if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
+        }
+        eq_run += half ? (uint32_t)__builtin_popcount(ehi) : e_lo_cnt;
       }
-      gt_run += __builtin_popcount(gm);
-      eq_run += __builtin_popcount(em);
     }
   }
   const uint32_t eq_taken = eq_run < need_eq ? eq_run : need_eq;
@@ -428,33 +456,37 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
 
   if (E > 1) {
     // k > 32: torch sorts the gathered picks stably by value, i.e. value
-    // descending then index ascending = descending order of the entries.
+    // descending then index ascending = descending order of the entries (all
+    // distinct but for the zero fill, so any correct sort gives the same order).
     // Bitonic sort (descending) of KP entries, E per lane, element e = hl*E + i.
+    // A compare-exchange is one med3 against a per-lane bound (all ones keeps the
+    // larger entry, zero the smaller); lanes exchange through DPP or ds_swizzle.
 #pragma unroll
     for (int k = 2; k <= KP; k <<= 1) {
 #pragma unroll
       for (int j = k >> 1; j > 0; j >>= 1) {
         if (j >= E) {
+          // (e & j) and (e & k) only depend on hl here (j, k >= E and E a power of 2).
           const int lj = j / E;
+          const bool lower = (hl & lj) == 0;
+          const bool desc = (hl & (k / E)) == 0;
+          const uint32_t bound = (lower == desc) ? 0xffffffffu : 0u;
 #pragma unroll
-          for (int i = 0; i < E; ++i) {
-            const uint32_t o = (uint32_t)__shfl_xor((int)sv[i], lj, 64);
-            const int e = hl * E + i;
-            const bool lower = (e & j) == 0;
-            const bool desc = (e & k) == 0;
-            const bool keep_max = (lower == desc);
-            sv[i] = keep_max ? (sv[i] > o ? sv[i] : o) : (sv[i] < o ? sv[i] : o);
-          }
+          for (int i = 0; i < E; ++i) sv[i] = med3_u32(sv[i], xor_lanes(sv[i], lj), bound);
         } else {
 #pragma unroll
           for (int i = 0; i < E; ++i) {
             if ((i & j) == 0) {
-              const int e = hl * E + i;
-              const bool desc = (e & k) == 0;
               const uint32_t x = sv[i], y = sv[i + j];
-              const bool swp = desc ? (x < y) : (x > y);
-              sv[i] = swp ? y : x;
-              sv[i + j] = swp ? x : y;
+              if (k < E) {  // direction fixed by i
+                const bool desc = (i & k) == 0;
+                sv[i] = desc ? max(x, y) : min(x, y);
+                sv[i + j] = desc ? min(x, y) : max(x, y);
+              } else {
+                const uint32_t bound = (hl & (k / E)) == 0 ? 0xffffffffu : 0u;
+                sv[i] = med3_u32(x, y, bound);
+                sv[i + j] = med3_u32(x, y, ~bound);
+              }
             }
           }
         }
