@@ -105,10 +105,21 @@ __device__ __forceinline__ uint32_t order_key16(uint32_t sc) {
   return u;
 }
 
-// Full wave over a 256-bin histogram (bins ascending in key): the bin b with
-// count(bins > b) < need <= count(bins >= b); gt = count(bins > b).
+// Full wave over a 256-bin histogram (bins ascending in key) kept as NC copies
+// kCopyStride words apart and summed here: the bin b with count(bins > b) < need <=
+// count(bins >= b); gt = count(bins > b).
+constexpr int kCopyStride = 260;  // 16-byte aligned; copy c's bin b is 4c banks off
+template <int NC = 1>
 __device__ __forceinline__ int find_bin64(const uint32_t* hist, int lane, uint32_t need, uint32_t& gt) {
-  const u32x4 v = *reinterpret_cast<const u32x4*>(hist + 4 * lane);
+  u32x4 v = *reinterpret_cast<const u32x4*>(hist + 4 * lane);
+#pragma unroll
+  for (int c = 1; c < NC; ++c) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(hist + c * kCopyStride + 4 * lane);
+    v[0] += w[0];
+    v[1] += w[1];
+    v[2] += w[2];
+    v[3] += w[3];
+  }
   const uint32_t local = v[0] + v[1] + v[2] + v[3];
   uint32_t incl = local;
 #pragma unroll
@@ -147,20 +158,33 @@ __device__ __forceinline__ void hist_add_grouped(uint32_t* hist, uint32_t bin, b
   }
 }
 
+// m & ~(b ^ s): the lanes of m whose ballot bit b equals the lane's own bit (s = 0
+// or ~0). One v_bitop3 (truth table 0x90) per call: the empty asm keeps the result
+// in a register, so that a chain of calls is not regrouped into xors and ors. (The
+// operation itself stays in C: the compiler inserts the wait states that a VALU
+// read of a ballot just written by a VALU compare needs, which it does not do for
+// inline assembly.)
+__device__ __forceinline__ uint32_t keep_equal(uint32_t m, uint32_t b, uint32_t s) {
+  uint32_t r = m & ~(b ^ s);
+  asm("" : "+v"(r));
+  return r;
+}
+
 // Stable sort, descending on the 8-bit digit (v >> sh) & 255, of the n values
 // src[0..n) into dst, by the NW waves (thread index tt) of a workgroup whose every
 // thread calls this. Wave w takes the w-th contiguous chunk in rounds of 64; per
 // round the lanes holding the same digit are found with one ballot per digit bit
-// that varies in the round, which gives each value its rank among equal digits
-// of the chunk so far (a per-wave running count per digit in wr). The digit
-// totals of all waves then give every (wave, digit) its output start.
+// (a lane keeps the ballot where its own bit is set, its complement where not:
+// m &= ~(ballot ^ sext(bit)), one v_bitop3 per half), which gives each value its
+// rank among equal digits of the chunk so far (a per-wave running count per digit
+// in wr). The digit totals of all waves then give every (wave, digit) its output
+// start. Inlined so that src, dst and wr are addressed as LDS.
 // wr: NW * 256 words, wt: NW words of LDS.
 template <int NW>
-__device__ void radix_pass_desc(const uint32_t* src, uint32_t* dst, int n, int sh, uint32_t* wr,
-                                uint32_t* wt, int tt) {
+__device__ __forceinline__ void radix_pass_desc(const uint32_t* src, uint32_t* dst, int n, int sh,
+                                                uint32_t* wr, uint32_t* wt, int tt) {
   constexpr int kR = kMaxK / (64 * NW);  // rounds per wave at most
   const int lane = tt & 63, wv = tt >> 6;
-  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
   const int chunk = ((n + NW - 1) / NW + 63) & ~63;
   const int c_beg = wv * chunk;
   const int c_end = min(n, c_beg + chunk);
@@ -175,19 +199,28 @@ __device__ void radix_pass_desc(const uint32_t* src, uint32_t* dst, int n, int s
     const uint32_t v = act ? src[c] : 0u;
     const uint32_t d = 255u - ((v >> sh) & 255u);
     const uint64_t am = __ballot(act);
-    uint64_t m = am;
+    uint32_t mlo = (uint32_t)am, mhi = (uint32_t)(am >> 32);
+    // equal digits <=> equal bits sh .. sh+7 of v; the eight ballots are all taken
+    // before they are used
+    uint32_t sx[8];
+    uint64_t bb[8];
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
-      const bool bit = (d >> b) & 1u;
-      const uint64_t bb = __ballot(act && bit);
-      if (bb != 0ull && bb != am) m &= bit ? bb : ~bb;  // uniform test: the bit varies
+      sx[b] = (uint32_t)__builtin_amdgcn_sbfe((int)v, sh + b, 1);  // 0 or ~0
+      asm("" : "+v"(sx[b]));  // the ballot tests sx itself (one compare)
+      bb[b] = __ballot(sx[b] != 0u);
     }
-    const uint32_t rank = (uint32_t)__builtin_popcountll(m & below);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      mlo = keep_equal(mlo, (uint32_t)bb[b], sx[b]);
+      mhi = keep_equal(mhi, (uint32_t)(bb[b] >> 32), sx[b]);
+    }
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
     uint32_t old = 0u;
     if (act) old = myw[d];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    if (act && rank == 0u) myw[d] = old + (uint32_t)__builtin_popcountll(m);
+    if (act && rank == 0u) myw[d] = old + (uint32_t)(__builtin_popcount(mlo) + __builtin_popcount(mhi));
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     vals[r] = v;
@@ -250,8 +283,9 @@ __device__ void radix_pass_desc(const uint32_t* src, uint32_t* dst, int n, int s
 // output (index + offset; -1 for picks beyond the valid candidates).
 // hist: max(512, NW * 256) words, sel: 4 words, sb and tmp: K words of LDS each.
 template <int NW>
-__device__ void select_topk_row(const uint16_t* keys, int nv, int K, uint32_t* hist, int32_t* sel,
-                                uint32_t* sb, uint32_t* tmp, int tt, int64_t* out_row, int64_t offset) {
+__device__ __forceinline__ void select_topk_row(const uint16_t* keys, int nv, int K, uint32_t* hist,
+                                                int32_t* sel, uint32_t* sb, uint32_t* tmp, int tt,
+                                                int64_t* out_row, int64_t offset) {
   constexpr int nthr = 64 * NW;
   const int lane = tt & 63;
   const int nw = NW, wv = tt >> 6;
@@ -598,8 +632,13 @@ struct SelParams {
 // NT threads per workgroup: 256 (32 keys per thread) for many rows, 1024 (8 keys per
 // thread) when there are too few rows to fill the CUs (decode), where the row's
 // latency is the step's.
+// The high-byte histogram is kept in kH1Copies copies (lane l adds to copy l % 4, so
+// that the lanes of one atomic instruction that hit the same bin, as the high bytes
+// of a row mostly do, are spread over 4 addresses), then the low-byte histogram.
+constexpr int kH1Copies = 4;
+constexpr int kH2 = kH1Copies * kCopyStride;  // offset of the low-byte histogram
 template <int NT>
-constexpr int sel_hist_words() { return (NT / 64) * 256 > 1024 ? (NT / 64) * 256 : 1024; }
+constexpr int sel_hist_words() { return (NT / 64) * 256 > kH2 + 256 ? (NT / 64) * 256 : kH2 + 256; }
 
 template <int NT>
 __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
@@ -640,19 +679,24 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
     const uint32_t w = (e & 2) ? kw[e >> 2].y : kw[e >> 2].x;
     return (e & 1) ? (w >> 16) : (w & 0xffffu);
   };
-  for (int i = tt; i < 512; i += NT) hist[i] = 0u;
+  // The histograms take whole 4-key pieces that start below nv: the 0 to 3 zero keys
+  // past nv in the last such piece fall into bin 0 of the high-byte histogram (and
+  // of the low-byte one when that bin is selected), which start at minus their
+  // number. (Every zero key past nv in one bin would serialise its atomics.)
+  const int npiece = min(max((nv - c0 + 3) >> 2, 0), KW);  // pieces of this thread
+  const uint32_t pad = (uint32_t)(((nv + 3) & ~3) - nv);
+  for (int i = tt; i < kH2 + 256; i += NT) hist[i] = (i == 0) ? 0u - pad : 0u;
   __syncthreads();
   uint32_t kth = 0u, n_gt = (uint32_t)nv, need_eq = 0u;
   if (selecting) {
+    uint32_t* h1 = hist + (lane & (kH1Copies - 1)) * kCopyStride;
 #pragma unroll
-    for (int e = 0; e < KPT; ++e) {
-      const uint32_t u = key_of(e);
-      if (u != 0u) atomicAdd(&hist[u >> 8], 1u);
-    }
+    for (int e = 0; e < KPT; ++e)
+      if ((e >> 2) < npiece) atomicAdd(&h1[key_of(e) >> 8], 1u);
     __syncthreads();
     if (wv == 0) {
       uint32_t gt;
-      const int b1 = find_bin64(hist, lane, (uint32_t)K, gt);
+      const int b1 = find_bin64<kH1Copies>(hist, lane, (uint32_t)K, gt);
       if (lane == 0) {
         sel[0] = b1;
         sel[1] = (int32_t)gt;
@@ -660,16 +704,17 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
     }
     __syncthreads();
     const uint32_t b1 = (uint32_t)sel[0];
+    if (b1 == 0u && tt == 0) atomicSub(&hist[kH2], pad);
 #pragma unroll
     for (int e = 0; e < KPT; ++e) {
       const uint32_t u = key_of(e);
-      if (u != 0u && (u >> 8) == b1) atomicAdd(&hist[256 + (u & 255u)], 1u);
+      if ((e >> 2) < npiece && (u >> 8) == b1) atomicAdd(&hist[kH2 + (u & 255u)], 1u);
     }
     __syncthreads();
     if (wv == 0) {
       uint32_t gt;
       const uint32_t above = (uint32_t)sel[1];
-      const int b0 = find_bin64(hist + 256, lane, (uint32_t)K - above, gt);
+      const int b0 = find_bin64(hist + kH2, lane, (uint32_t)K - above, gt);
       if (lane == 0) {
         sel[2] = b0;
         sel[3] = (int32_t)(above + gt);
@@ -701,17 +746,25 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   __syncthreads();
   uint32_t base = incl - cnt;
   for (int w = 0; w < wv; ++w) base += wt[w];
-  uint32_t og = base & 0xffffu, oe = base >> 16;
+  uint32_t og = base & 0xffffu, oe = n_gt + (base >> 16);  // next slots of each kind
+  const uint32_t oe_end = n_gt + need_eq;
+  const uint32_t ibase = 0xffffu - (uint32_t)c0;
+  // The comparisons are recomputed below rather than kept from the count loop (64
+  // lane masks of it would not fit in the scalar registers).
+#pragma unroll
+  for (int i = 0; i < KW; ++i) asm volatile("" : "+v"(kw[i]));
 #pragma unroll
   for (int e = 0; e < KPT; ++e) {
     const uint32_t u = key_of(e);
-    const uint32_t comp = (u << 16) | (0xffffu - (uint32_t)(c0 + e));
-    if (u > kth) {
-      sortbuf[og++] = comp;
-    } else if (u == kth_e) {
-      if (oe < need_eq) sortbuf[n_gt + oe] = comp;
-      ++oe;
-    }
+    const bool g = u > kth, q = u == kth_e;
+    const bool ok = g | (q & (oe < oe_end));
+    const uint32_t pos = g ? og : oe;
+    // (u << 16) | (index bits): one v_perm of the key's 16-bit half and ibase - e
+    const uint32_t w = (e & 2) ? kw[e >> 2].y : kw[e >> 2].x;
+    const uint32_t comp = __builtin_amdgcn_perm(w, ibase - (uint32_t)e, (e & 1) ? 0x07060100u : 0x05040100u);
+    if (ok) sortbuf[pos] = comp;
+    og += g ? 1u : 0u;
+    oe += q ? 1u : 0u;
   }
   const int count = selecting ? K : nv;
   __syncthreads();
