@@ -50,10 +50,11 @@ struct MlaParams {
   const float* sink;     // [H]
   uint16_t* out;         // [B, M, H, 512]
   int64_t M;
-  float* part;           // split mode: [B*M, nsplit, H, 512] fp32 unnormalised O^T rows ...
+  float* part;           // split mode: [B*M, nsplit, H/16 waves, 32 tiles, 64 lanes, 4] fp32 O^T ...
   float* ml;             // ... and [B*M, nsplit, H, 2] (running max, log2 domain; sum); else null
-  int32_t nsplit;        // workgroups per token (1: the whole slot list, bf16 output)
+  int32_t nsplit;        // slot ranges per token (1: the whole slot list, bf16 output)
   int32_t bps;           // slot blocks per split
+  int32_t hg;            // split mode: head groups per token (workgroups of 16 NW heads)
   int32_t B, H, NKV, TOPK, kv_dim;
   float scale_log2;
 };
@@ -76,8 +77,12 @@ void sa_mla_kernel(MlaParams p) {
   int32_t* nblk_sh = slot + nblk * kKB;  // [NW] blocks up to each wave's last valid slot
   // Split mode: workgroup (token, sp) takes slot blocks [kb0, kb0 + nbl) of the token;
   // `slot` and the block numbers kb below count from kb0.
-  const int64_t tok = kSplit ? (int64_t)(blockIdx.x / p.nsplit) : (int64_t)blockIdx.x;
-  const int sp = kSplit ? (int)(blockIdx.x % p.nsplit) : 0;
+  // Split mode: workgroup ((token * nsplit + sp) * hg + hgi) takes the 16 NW heads of
+  // head group hgi.
+  const int hgi = kSplit ? (int)(blockIdx.x % p.hg) : 0;
+  const int64_t tsp = kSplit ? (int64_t)(blockIdx.x / p.hg) : 0;
+  const int64_t tok = kSplit ? tsp / p.nsplit : (int64_t)blockIdx.x;
+  const int sp = kSplit ? (int)(tsp % p.nsplit) : 0;
   const int kb0 = kSplit ? sp * p.bps : 0;
   const int nbl = kSplit ? max(0, min(p.bps, nblk - kb0)) : nblk;
 
@@ -87,7 +92,7 @@ void sa_mla_kernel(MlaParams p) {
   const int b = (int)(tok / p.M);
   const int n = lane & 15;  // head 16wi + n
   const int g = lane >> 4;  // lane group: k-slice 8g..8g+7, C rows 4g..4g+3
-  const int head = 16 * wi + n;
+  const int head = 16 * (NW * hgi + wi) + n;
 
   // The token's global reads (Q^T, the sink, the slot indices) are all issued
   // before any of them is waited for. Q^T fragments (B operand): head `head`,
@@ -348,13 +353,18 @@ void sa_mla_kernel(MlaParams p) {
   l_run += __shfl_xor(l_run, 32, 64);
   if constexpr (kSplit) {
     // Split mode: this range's state relative to its running max m_run (the sink is
-    // applied once, by sa_mla_combine_kernel). Lane (n, g) holds channels
-    // 16ct + 4g .. +3 of head 16wi + n.
-    const int64_t prow = (tok * p.nsplit + sp) * p.H + head;
-    float* dstp = p.part + prow * kDV + 4 * g;
+    // applied once, by sa_mla_combine_kernel). O^T goes out in register order, per
+    // (token, split, wave) 32 tiles of 64 lanes x 16 B, so that every store writes
+    // 1 KB contiguously; lane (n, g) of tile ct holds channels 16ct + 4g .. +3 of
+    // head 16(NW hgi + wi) + n.
+    const int64_t pw = (tok * p.nsplit + sp) * (p.H >> 4) + NW * hgi + wi;
+    f32x4* dstp = reinterpret_cast<f32x4*>(p.part) + pw * (kCT * 64) + lane;
 #pragma unroll
-    for (int ct = 0; ct < kCT; ++ct) *reinterpret_cast<f32x4*>(dstp + 16 * ct) = o[ct];
-    if (g == 0) *reinterpret_cast<float2*>(p.ml + prow * 2) = make_float2(m_run, l_run);
+    for (int ct = 0; ct < kCT; ++ct) dstp[ct * 64] = o[ct];
+    if (g == 0) {
+      const int64_t prow = (tok * p.nsplit + sp) * p.H + head;
+      *reinterpret_cast<float2*>(p.ml + prow * 2) = make_float2(m_run, l_run);
+    }
     return;
   }
   const float rz = 1.0f / (l_run + __builtin_amdgcn_exp2f(sink_l2 - m_run));
@@ -383,34 +393,42 @@ constexpr int kMaxSplit = 32;  // splits per token at most (the combine keeps th
 
 // Split mode's second step: per (token, head) row, M = max(sink, m_i),
 // Z = exp2(sink - M) + sum_i l_i exp2(m_i - M), out = bf16(sum_i O_i exp2(m_i - M) / Z).
-// One workgroup of 256 threads per two rows, 4 channels per thread.
+// One thread per (token, wave, tile, lane) of the split kernel's register layout
+// (head 16 wave + lane % 16, channels 16 tile + 4 (lane / 16) .. +3), so that each
+// split's partial is read 1 KB per wave instruction. One wave per workgroup: a
+// token's 16 K threads then spread over 256 CUs (each thread reads 16 B of every
+// split, 512 B for 32 splits).
 struct MlaCombineParams {
   const float* part;
   const float* ml;
   const float* sink;
   uint16_t* out;
-  int64_t rows;  // B * M * H
+  int64_t n;  // threads: B * M * H * 128
   int32_t H, nsplit;
 };
 
-__global__ __launch_bounds__(256) void sa_mla_combine_kernel(MlaCombineParams p) {
-  const int64_t row = (int64_t)blockIdx.x * 2 + (threadIdx.x >> 7);
-  if (row >= p.rows) return;
-  const int c4 = threadIdx.x & 127;
-  const int head = (int)(row % p.H);
-  const int64_t tok = row / p.H;
+__global__ __launch_bounds__(64) void sa_mla_combine_kernel(MlaCombineParams p) {
+  const int64_t f = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (f >= p.n) return;
+  const int lane = (int)(f & 63);
+  const int ct = (int)((f >> 6) & (kCT - 1));
+  const int nwv = p.H >> 4;  // waves per token in the split kernel
+  const int64_t tw = f >> 11;  // token * nwv + wave
+  const int64_t tok = tw / nwv;
+  const int w = (int)(tw - tok * nwv);
+  const int head = 16 * w + (lane & 15), g = lane >> 4;
   const float sink_l2 = p.sink[head] * kLog2e;
-  const int64_t r0 = tok * p.nsplit * p.H + head;  // partial row of split 0
-  // Splits in groups of 8 whose loads are all issued before any is used (the
-  // host caps nsplit at kMaxSplit).
+  const f32x4* part = reinterpret_cast<const f32x4*>(p.part);
+  // All splits' loads are issued before any is used (the host caps nsplit at
+  // kMaxSplit).
   float2 ml[kMaxSplit];
   f32x4 v[kMaxSplit];
 #pragma unroll
   for (int i = 0; i < kMaxSplit; ++i) {
     if (i < p.nsplit) {
-      const int64_t ri = r0 + (int64_t)i * p.H;
-      ml[i] = *reinterpret_cast<const float2*>(p.ml + ri * 2);
-      v[i] = *reinterpret_cast<const f32x4*>(p.part + ri * kDV + 4 * c4);
+      const int64_t ts = tok * p.nsplit + i;
+      ml[i] = *reinterpret_cast<const float2*>(p.ml + (ts * p.H + head) * 2);
+      v[i] = part[((ts * nwv + w) * kCT + ct) * 64 + lane];
     }
   }
   float mx = sink_l2;
@@ -422,17 +440,17 @@ __global__ __launch_bounds__(256) void sa_mla_combine_kernel(MlaCombineParams p)
 #pragma unroll
   for (int i = 0; i < kMaxSplit; ++i) {
     if (i < p.nsplit) {
-      const float w = __builtin_amdgcn_exp2f(ml[i].x - mx);
-      z += ml[i].y * w;
+      const float wgt = __builtin_amdgcn_exp2f(ml[i].x - mx);
+      z += ml[i].y * wgt;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] += v[i][r] * w;
+      for (int r = 0; r < 4; ++r) acc[r] += v[i][r] * wgt;
     }
   }
   const float rz = 1.0f / z;
   uint2 pk;
   pk.x = pack_bf2(acc[0] * rz, acc[1] * rz);
   pk.y = pack_bf2(acc[2] * rz, acc[3] * rz);
-  *reinterpret_cast<uint2*>(p.out + row * kDV + 4 * c4) = pk;
+  *reinterpret_cast<uint2*>(p.out + (tok * p.H + head) * kDV + 16 * ct + 4 * g) = pk;
 }
 
 // Split plan: with fewer tokens than CUs, each token's slot blocks are divided
@@ -457,7 +475,7 @@ int64_t mla_split_bytes(int64_t tokens, int64_t h, int nsplit) {
 
 template <typename IdxT, bool kSplit>
 int mla_launch(const MlaParams& p, int nw, size_t smem, hipStream_t st) {
-  const dim3 grid((unsigned)((int64_t)p.B * p.M * p.nsplit));
+  const dim3 grid((unsigned)((int64_t)p.B * p.M * p.nsplit * p.hg));
   switch (nw) {
 #define DSA_MLA_CASE(n)                                                                           \
   case n:                                                                                         \
@@ -515,6 +533,7 @@ int sparse_mla_fwd(const void* q, const void* kv, const void* topk_idxs, bool id
   p.ml = nullptr;
   p.nsplit = 1;
   p.bps = (int32_t)nblk;
+  p.hg = 1;
   if (workspace != nullptr) {
     int cu = 0;
     if (dsa_host::device_cu_count(&cu) != DSA_OK) return DSA_ERR_DEVICE;
@@ -528,11 +547,15 @@ int sparse_mla_fwd(const void* q, const void* kv, const void* topk_idxs, bool id
       p.ml = p.part + b * m * nsplit * h * kDV;
       p.nsplit = nsplit;
       p.bps = bps;
+      // Two head groups of 4 waves when 128 heads' workgroups would still leave most
+      // CUs idle: each workgroup then reads half the token's queries and writes half
+      // the partials, and twice as many CUs share the work.
+      if (h / 32 >= 4 && b * m * nsplit * 2 <= cu) p.hg = 2;
     }
   }
   const size_t smem = (size_t)kRingM * kBlkBytes + (size_t)nblk * kKB * 4 + 32;  // + per-wave counts
   hipStream_t st = (hipStream_t)stream;
-  const int nw = (int)(h / 16);
+  const int nw = (int)(h / 16) / p.hg;
   int rc;
   if (p.nsplit > 1)
     rc = idx64 ? mla_launch<int64_t, true>(p, nw, smem, st) : mla_launch<int32_t, true>(p, nw, smem, st);
@@ -544,10 +567,10 @@ int sparse_mla_fwd(const void* q, const void* kv, const void* topk_idxs, bool id
   c.ml = p.ml;
   c.sink = attn_sink;
   c.out = (uint16_t*)out;
-  c.rows = b * m * h;
+  c.n = b * m * h * 128;
   c.H = (int32_t)h;
   c.nsplit = p.nsplit;
-  hipLaunchKernelGGL(sa_mla_combine_kernel, dim3((unsigned)((c.rows + 1) / 2)), dim3(256), 0, st, c);
+  hipLaunchKernelGGL(sa_mla_combine_kernel, dim3((unsigned)((c.n + 63) / 64)), dim3(64), 0, st, c);
   return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_LAUNCH;
 }
 
