@@ -32,6 +32,24 @@ def _compare(out, ref, name, atol=1e-2, rtol=1e-2):
     return exact
 
 
+def _compare_all_tokens(out, q, kv, sink, idx, scale, name, chunk=256):
+    """_compare over every token of out[1, M, ...] with the oracle run on `chunk` tokens at
+    a time (the oracle's gathered rows for all 8192 configs[4] tokens would be ~40 GB).
+    Returns the fraction of bit-identical outputs."""
+    m = out.shape[1]
+    n_exact, n_all = 0.0, 0
+    for i in range(0, m, chunk):
+        sl = slice(i, min(m, i + chunk))
+        ref = osa.sparse_attn_ref(q[:, sl], kv, sink, idx[:, sl], scale, v_dim=DV)
+        e = _compare(out[:, sl], ref, f"{name} tokens {sl.start}..{sl.stop - 1}")
+        n_exact += e * ref.numel()
+        n_all += ref.numel()
+        del ref
+    exact = n_exact / n_all
+    _say(f"[{name}] all {m} tokens: bit-exact {exact:.6f}")
+    return exact
+
+
 def _case(b, m, h, n_kv, topk, seed, masked=0.0, sink_scale=0.0, kv_dim=DQK, dev="cuda"):
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(b, m, h, DQK, generator=g).to(torch.bfloat16)
@@ -162,20 +180,18 @@ def test_mla_drop_in_module(gpu):
     _compare(out, ref, "mla-module")
 
 
-def test_full_shape_c5_mla_sampled(gpu):
-    """configs[4] attention: q[1,8192,128,576], kv[1,8192,576], top-2048 causal picks. The
-    kernel runs on the whole shape; the oracle checks every 32nd token (and the last)."""
+def test_full_shape_c5_mla(gpu):
+    """configs[4] attention: q[1,8192,128,576], kv[1,8192,576], top-2048 causal picks
+    (t1.get_mla_inputs). The kernel runs on the whole shape; the oracle checks all 8192
+    tokens, 256 at a time."""
     _say("case c5 mla inputs")
     q, kv, idx = t1.get_mla_inputs(device=gpu)
     sink = torch.zeros(128, device=gpu)
     _say("case c5 mla kernel")
     out = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV)
     torch.cuda.synchronize()
-    rows = torch.cat([torch.arange(0, 8192, 32), torch.tensor([8191])]).to(gpu)
     _say("case c5 mla oracle")
-    ref = torch.cat([osa.sparse_attn_ref(q[:, rows[i:i + 32]], kv, sink, idx[:, rows[i:i + 32]], SCALE, v_dim=DV)
-                     for i in range(0, len(rows), 32)], dim=1)
-    exact = _compare(out[:, rows], ref, "c5-mla")
+    exact = _compare_all_tokens(out, q, kv, sink, idx, SCALE, "c5-mla")
     assert exact > 0.97
 
 
@@ -211,8 +227,8 @@ def test_dsa_layer_c5_full_size_chained(gpu):
     """configs[4] prefill chained as in the reference (task2_v0_ref.py:138-143 output is
     task1_v0_ref.py:8-12's topk_idxs): the indexer Model.forward at 8192 tokens with
     W ~ N(0, 0.02) gives int64 top-2048 picks equal to the oracle's on the same GPU; they
-    go unchanged into Model(128, 576, v_dim=512), whose output is checked on every 32nd
-    token (and the last) against the oracle's attention over the same picks."""
+    go unchanged into Model(128, 576, v_dim=512), whose output is checked on all 8192
+    tokens against the oracle's attention over the same picks (in chunks of 256 tokens)."""
     torch.manual_seed(42)
     init = t2.get_c5_init_inputs(device=gpu)
     ix = t2.Model(*init).to(gpu)
@@ -240,9 +256,6 @@ def test_dsa_layer_c5_full_size_chained(gpu):
     _say("case c5 chained: sparse MLA over the indexer's picks")
     out = attn(qm, kvm, picks)
     torch.cuda.synchronize()
-    rows = torch.cat([torch.arange(0, 8192, 32), torch.tensor([8191])]).to(gpu)
-    _say("case c5 chained: oracle attention")
-    ref = torch.cat([osa.sparse_attn_ref(qm[:, rows[i:i + 32]], kvm, attn.attn_sink, picks[:, rows[i:i + 32]],
-                                         attn.softmax_scale, v_dim=DV) for i in range(0, len(rows), 32)], dim=1)
-    exact = _compare(out[:, rows], ref, "c5-chained")
+    _say("case c5 chained: oracle attention over all 8192 tokens")
+    exact = _compare_all_tokens(out, qm, kvm, attn.attn_sink, picks, attn.softmax_scale, "c5-chained")
     assert exact > 0.97
