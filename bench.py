@@ -7,7 +7,7 @@ replacement), inputs resident in HBM. One step = one forward call of the drop-in
 module (one kernel launch). value = algorithmic HBM bytes per call / time per call.
 
 Also reported, each with hot-cache times and times with the 256 MB MALL flushed
-(512 MB written before every call):
+(512 MB written and read back before every call):
   task1_c1      configs[0] on the GPU, beside the reference path on the host CPU;
   task1_c4      the true-gather kernel at configs[3] (MFMA-bound);
   task2         configs[2]: Model.forward (query projection + RoPE kernel, the
@@ -87,10 +87,14 @@ def _warm(torch, fn, steps, min_seconds=0.3):
 
 
 def _cold_time(torch, fn, reps, stream, flush):
-    """Median ms per call with the 256 MB MALL flushed (512 MB written) before every call."""
+    """Median ms per call with the 256 MB MALL flushed before every call: 512 MB are
+    written, then read back, so that the caches hold only clean lines of the flush buffer
+    (with the write alone, its dirty lines would be written back to HBM during the timed
+    call and be counted against the kernel)."""
     ts = []
     for _ in range(reps):
         flush.fill_(1)
+        flush.view(torch.int64).sum()
         a = torch.cuda.Event(enable_timing=True)
         z = torch.cuda.Event(enable_timing=True)
         a.record(stream)
