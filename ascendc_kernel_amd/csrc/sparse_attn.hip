@@ -12,8 +12,9 @@
 // src/sparse_attn_kernel_mm.asc:155-292). Each wave streams 16-row tiles
 // (16 heads of one token) straight from HBM into MFMA operands:
 //   S^T[32 x 16]  = KV[32 x 128] . Q^T[128 x 16]        (8 x mfma 16x16x32)
-//   P             = c_j * exp(S - M) / Z, fp32, split hi + lo bf16
-//   O^T[128 x 16] = KV^T[128 x 32] . (P_hi + P_lo)^T    (16 x mfma 16x16x32)
+//   P             = c_j * exp(S - M) / Z, fp32, split into three bf16 terms
+//                   P_hi + P_lo + P_lo2 (together all 24 bits of P)
+//   O^T[128 x 16] = KV^T[128 x 32] . (P_lo2 + P_lo + P_hi)^T  (24 x mfma 16x16x32)
 // The kv block of the current batch lives in registers in both operand
 // layouts, so S and P never leave the CU. The contraction indices of both
 // products are permuted (pi over kv rows, delta over channels) so that the
@@ -261,23 +262,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     z += shfl_xor_f(z, 32);
     z += __expf(sk - mrow);
     const float rz = __builtin_amdgcn_rcpf(z);
-    u32x4 whi, wlo;
+    // P = hi + lo + lo2: hi = bf16(p), lo = bf16(p - hi), lo2 = bf16(p - hi - lo)
+    // (both differences exact in fp32). With two terms P kept ~16 bits and 0.19 %
+    // of the configs[1] outputs differed from the reference's fp32 path by one
+    // bf16 ulp; with three, 0.011 %. The third products are free here: the
+    // kernel is bound by HBM, its matrix cores ~10 % busy.
+    u32x4 whi, wlo, wlo2;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const float p0 = e[2 * w] * rz, p1 = e[2 * w + 1] * rz;
       const uint32_t h = pack_bf2(p0, p1);
       whi[w] = h;
-      wlo[w] = pack_bf2(p0 - bf_lo(h), p1 - bf_hi(h));
+      const float r0 = p0 - bf_lo(h), r1 = p1 - bf_hi(h);
+      const uint32_t l = pack_bf2(r0, r1);
+      wlo[w] = l;
+      wlo2[w] = pack_bf2(r0 - bf_lo(l), r1 - bf_hi(l));
     }
     const bf16x8 phi = __builtin_bit_cast(bf16x8, whi);
     const bf16x8 plo = __builtin_bit_cast(bf16x8, wlo);
+    const bf16x8 plo2 = __builtin_bit_cast(bf16x8, wlo2);
 
-    // O^T = KV^T . P^T, low part first then high part into the same accumulator.
+    // O^T = KV^T . P^T, smallest part first, into one accumulator.
     f32x4 o[8];
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       const bf16x8 a = __builtin_bit_cast(bf16x8, img_pv[mt][lane]);
-      o[mt] = mfma16x16x32(a, plo, f32x4{0.f, 0.f, 0.f, 0.f});
+      o[mt] = mfma16x16x32(a, plo2, f32x4{0.f, 0.f, 0.f, 0.f});
+      o[mt] = mfma16x16x32(a, plo, o[mt]);
       o[mt] = mfma16x16x32(a, phi, o[mt]);
     }
     // Transpose the tile through LDS so every store instruction writes four

@@ -54,7 +54,9 @@ def test_full_shape_c2(gpu, seed):
     ref = osa.sparse_attn_ref(q, kv, m.attn_sink, idx, m.softmax_scale)
     torch.cuda.synchronize()
     exact = _compare(out, ref, "c2")
-    assert exact > 0.99
+    # P enters the PV product as three bf16 terms (all 24 bits): 99.989 % of the outputs
+    # equal the fp32 path's bit for bit (99.81 % with two terms).
+    assert exact > 0.9995
     out2 = m(q, kv, idx)
     assert torch.equal(out, out2), "not deterministic"
 
