@@ -291,18 +291,29 @@ void sa_mla_kernel(MlaParams p) {
     for (int r = 0; r < 8; ++r) pe[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], c2, -m_run));
 #pragma unroll
     for (int r = 0; r < 8; ++r) l_run += pe[r];
-    u32x4 wh, wl;
+    // P = hi + lo (~16 bits) or, in split mode, hi + lo + lo2 (all 24 bits): the split
+    // kernel's workgroups each take a few blocks (latency-bound), where the third
+    // products cost nothing measurable; in the one-pass kernel they would cost ~23 %.
+    u32x4 wh, wl, wl2;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const float p0 = pe[2 * w], p1 = pe[2 * w + 1];
       const uint32_t h = pack_bf2(p0, p1);
       wh[w] = h;
       const bf16v2 hv = __builtin_bit_cast(bf16v2, h);
-      wl[w] = pack_bf2(__builtin_amdgcn_fdot2_f32_bf16(hv, neg_lo, p0, false),
-                       __builtin_amdgcn_fdot2_f32_bf16(hv, neg_hi, p1, false));
+      const float r0 = __builtin_amdgcn_fdot2_f32_bf16(hv, neg_lo, p0, false);
+      const float r1 = __builtin_amdgcn_fdot2_f32_bf16(hv, neg_hi, p1, false);
+      const uint32_t l = pack_bf2(r0, r1);
+      wl[w] = l;
+      if constexpr (kSplit) {
+        const bf16v2 lv = __builtin_bit_cast(bf16v2, l);
+        wl2[w] = pack_bf2(__builtin_amdgcn_fdot2_f32_bf16(lv, neg_lo, r0, false),
+                          __builtin_amdgcn_fdot2_f32_bf16(lv, neg_hi, r1, false));
+      }
     }
     const bf16x8 phi = __builtin_bit_cast(bf16x8, wh);
     const bf16x8 plo = __builtin_bit_cast(bf16x8, wl);
+    const bf16x8 plo2 = __builtin_bit_cast(bf16x8, wl2);
     // O^T += V^T . P^T: supplier lane s = lane%16 of group g reads 4 channels
     // 16ct + 4(s%4) .. +3 of key row 4g + s/4 (first read) and 16 + 4g + s/4
     // (second); the transposed reads hand channel 16ct + (lane%16) keys
@@ -323,17 +334,19 @@ void sa_mla_kernel(MlaParams p) {
     for (int ct = 0; ct < kCT; ++ct) {
       bf16x8 a_nxt = a_cur;
       if (ct + 1 < kCT) a_nxt = read_v(ct + 1);
+      if constexpr (kSplit) o[ct] = mfma16x16x32(a_cur, plo2, o[ct]);
       o[ct] = mfma16x16x32(a_cur, plo, o[ct]);
       o[ct] = mfma16x16x32(a_cur, phi, o[ct]);
       a_cur = a_nxt;
     }
+    constexpr int kPv = kSplit ? 3 : 2;  // products per V^T fragment
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
     for (int ct = 0; ct < kCT - 1; ++ct) {
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, kPv, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, kPv, 0);
     vm_cur = vm_next;
   };
 
