@@ -613,10 +613,12 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
 }
 
 // Top-K of rows of 16-bit order keys written by ix_wide_kernel: one workgroup
-// (256 threads) per token row. Thread tt holds keys [32 tt, 32 tt + 32) of the row
-// in registers (index order = thread order, then register order):
-//   1. high-byte histogram (LDS atomics), the bin of the K-th key; low-byte
-//      histogram of that bin, the K-th key itself (kth) and n_gt = #(keys > kth);
+// (256 threads, or 1024 for few rows) per token row. Thread tt holds keys
+// [KPT tt, KPT tt + KPT) of the row in registers (index order = thread order, then
+// register order):
+//   1. high-byte histogram (LDS atomics into 4 lane-interleaved copies), the bin of
+//      the K-th key; low-byte histogram of that bin, the K-th key itself (kth) and
+//      n_gt = #(keys > kth);
 //   2. one workgroup scan of the per-thread counts (#(> kth) | #(== kth) << 16)
 //      places every pick: [> kth] at [0, n_gt) and the first K - n_gt [== kth]
 //      after them, each in index order;
