@@ -57,9 +57,12 @@ def _settled_us(fn, reps, min_seconds=0.3):
 
 
 # Kernel-time budgets in microseconds (hot caches, settled clock): a regression of the
-# kernels past these fails. Measured values are printed.
-BUDGET_US = {"c2": 125.0, "c3_kernel": 55.0, "c3_q_proj": 24.0, "c3_model": 82.0, "c4": 420.0,
-             "c5_mla": 5500.0}
+# kernels past these fails. Measured values are printed. Each sits ~7-15 % above the
+# slowest box of the pool seen so far (C2 117-120, C3 kernel with in-kernel RoPE 48-51,
+# projection 18-20, Model.forward 73-76, C4 383-423, C5 sparse MLA 5,070-5,700 us), so
+# that box-to-box spread alone does not fail the suite.
+BUDGET_US = {"c2": 128.0, "c3_kernel": 58.0, "c3_q_proj": 23.0, "c3_model": 84.0, "c4": 470.0,
+             "c5_mla": 6300.0}
 
 
 def test_budget_task1_c2(gpu):
