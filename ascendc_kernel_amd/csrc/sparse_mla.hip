@@ -143,25 +143,32 @@ void sa_mla_kernel(MlaParams p) {
                                (uint32_t)p.NKV * (uint32_t)p.kv_dim * 2u);
   const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;
   const uint32_t row_bytes = (uint32_t)p.kv_dim * 2u;
-  auto rows_of = [&](int blk, int (&rv)[kUnitsW]) {
+  // Copy offsets of block blk for this wave's units. They are recomputed from the
+  // lane id at every use: an opaque copy of the id keeps the compiler from holding
+  // ten per-lane values in registers across the block loop (which spilled them and
+  // put a scratch reload, with its vmcnt(0) wait on the copies in flight, into the
+  // loop).
+  auto rows_of = [&](int blk, uint32_t (&rv)[kUnitsW]) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int i = 0; i < kUnitsW; ++i) {
       int u = wis + NW * i;
       if (u >= kUnitsBlk) u = kUnitsBlk - 1;
-      const int r = (64 * u + lane) / kRowC;
-      rv[i] = r < kKB ? slot[blk * kKB + r] : -1;
+      const int pos = 64 * u + ln;
+      const int r = pos / kRowC;
+      const int c = pos - r * kRowC;
+      const int w = slot[blk * kKB + min(r, kKB - 1)];
+      rv[i] = (r < kKB && w >= 0 && c < kRowC - 1) ? (uint32_t)w * row_bytes + 16u * (uint32_t)c : kOob;
     }
   };
-  auto issue = [&](int blk, const int (&rv)[kUnitsW]) {
+  auto issue = [&](int blk, const uint32_t (&rv)[kUnitsW]) {
     const uint32_t base = ring_lds + (uint32_t)(blk % kRingM) * (uint32_t)kBlkBytes;
 #pragma unroll
     for (int i = 0; i < kUnitsW; ++i) {
       int u = wis + NW * i;
       if (u >= kUnitsBlk) u = kUnitsBlk - 1;
-      const int c = (64 * u + lane) % kRowC;
-      const uint32_t voff =
-          (rv[i] >= 0 && c < kRowC - 1) ? (uint32_t)rv[i] * row_bytes + 16u * (uint32_t)c : kOob;
-      lds_dma16(rsrc, voff, base + 1024u * (uint32_t)u);
+      lds_dma16(rsrc, rv[i], base + 1024u * (uint32_t)u);
     }
   };
 
@@ -208,7 +215,7 @@ void sa_mla_kernel(MlaParams p) {
 #pragma unroll
   for (int j = 0; j < kRingM - 1; ++j) {
     if (j < nb) {
-      int rv[kUnitsW];
+      uint32_t rv[kUnitsW];
       rows_of(j, rv);
       issue(j, rv);
     }
@@ -239,7 +246,7 @@ void sa_mla_kernel(MlaParams p) {
       else wait_vmcnt<0>();
       __syncthreads();  // block kb+1 is in LDS; block kb-1's buffer is free
       if (kb + kRingM - 1 < nb) {
-        int rv[kUnitsW];
+        uint32_t rv[kUnitsW];
         rows_of(kb + kRingM - 1, rv);
         issue(kb + kRingM - 1, rv);
       }
