@@ -7,7 +7,9 @@ replacement), inputs resident in HBM. One step = one forward call of the drop-in
 module (one kernel launch). value = algorithmic HBM bytes per call / time per call.
 
 Also reported, each with hot-cache times and times with the 256 MB MALL flushed
-(512 MB written and read back before every call):
+(512 MB written and read back before every call; back-to-back flush + call pairs
+minus the flushes alone, so that cold and hot calls are timed the same way; the
+headline also gives one call timed alone after a flush):
   task1_c1      configs[0] on the GPU, beside the reference path on the host CPU;
   task1_c4      the true-gather kernel at configs[3] (MFMA-bound);
   task2         configs[2]: Model.forward (query projection + RoPE kernel, the
@@ -86,15 +88,43 @@ def _warm(torch, fn, steps, min_seconds=0.3):
         torch.cuda.synchronize()
 
 
+def _flush(torch, flush):
+    """Evicts the 256 MB MALL: 512 MB are written, then read back, so that the caches hold
+    only clean lines of the flush buffer (with the write alone, its dirty lines would be
+    written back to HBM during the next call and be counted against it)."""
+    flush.fill_(1)
+    flush.view(torch.int64).sum()
+
+
 def _cold_time(torch, fn, reps, stream, flush):
-    """Median ms per call with the 256 MB MALL flushed before every call: 512 MB are
-    written, then read back, so that the caches hold only clean lines of the flush buffer
-    (with the write alone, its dirty lines would be written back to HBM during the timed
-    call and be counted against the kernel)."""
+    """Ms per call with the MALL flushed before every call, timed like the hot figure:
+    `reps` back-to-back (flush, call) pairs minus `reps` flushes alone, median of 5 such
+    differences. Each call then follows other work on the stream, as in the hot loop, so
+    the two figures differ only by what the flush evicted."""
+    d = []
+    for _ in range(5):
+        t = []
+        for with_call in (True, False):
+            a = torch.cuda.Event(enable_timing=True)
+            z = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(reps):
+                _flush(torch, flush)
+                if with_call:
+                    fn()
+            z.record(stream)
+            z.synchronize()
+            t.append(a.elapsed_time(z))
+        d.append((t[0] - t[1]) / reps)
+    return statistics.median(d)
+
+
+def _cold_single_time(torch, fn, reps, stream, flush):
+    """Median ms of one call timed alone (its own event pair) right after a flush: this
+    also counts the call's dispatch, which back-to-back calls overlap."""
     ts = []
     for _ in range(reps):
-        flush.fill_(1)
-        flush.view(torch.int64).sum()
+        _flush(torch, flush)
         a = torch.cuda.Event(enable_timing=True)
         z = torch.cuda.Event(enable_timing=True)
         a.record(stream)
@@ -185,6 +215,9 @@ def main():
     def cold(fn, reps):
         return None if flush is None else round(_cold_time(torch, fn, reps, stream, flush) * 1e3, 2)
 
+    def cold_single(fn, reps):
+        return None if flush is None else round(_cold_single_time(torch, fn, reps, stream, flush) * 1e3, 2)
+
     # ---------------- Task1 headline; the CPU copies of the inputs are kept
     # for the host-CPU reference leg.
     torch.manual_seed(42)
@@ -195,7 +228,8 @@ def main():
         _warm(torch, lambda: model(q, kv, idx), a.warmup)
         ms = _events_time(torch, lambda: model(q, kv, idx), a.steps, stream)
         torch.cuda.synchronize()
-        c2_cold = cold(lambda: model(q, kv, idx), 10)
+        c2_cold = cold(lambda: model(q, kv, idx), 20)
+        c2_cold_single = cold_single(lambda: model(q, kv, idx), 21)
         # The same bytes moved by torch's device copy (q read once, one output written).
         cpy = torch.empty_like(q)
         _warm(torch, lambda: cpy.copy_(q), 3, 0.1)
@@ -231,6 +265,7 @@ def main():
         "roofline": _roofline_hbm(nb, ms, _traffic("sa_mult_kernel")),
         "traffic_source": TRAFFIC_SOURCE,
         "cold_mall_us_per_call": c2_cold,
+        "cold_mall_single_call_us": c2_cold_single,
         "torch_copy_same_bytes": {"us": round(ms_copy * 1e3, 2),
                                   "GBps": round(2 * q.numel() * 2 / (ms_copy * 1e-3) / 1e9, 1)},
     }
@@ -247,7 +282,7 @@ def main():
     with torch.no_grad():
         _warm(torch, lambda: model(q1, kv1, idx1), 10, 0.1)
         ms1 = _events_time(torch, lambda: model(q1, kv1, idx1), max(20, a.steps), stream)
-        c1_cold = cold(lambda: model(q1, kv1, idx1), 10)
+        c1_cold = cold(lambda: model(q1, kv1, idx1), 40)
     result["task1_c1"] = {
         "workload": "task1 configs[0]: q[1,160,64,128] bf16, kv[1,32,128], topk_idxs[1,160,16] with replacement",
         "us_per_call": round(ms1 * 1e3, 2), "cold_mall_us_per_call": c1_cold,
@@ -263,7 +298,7 @@ def main():
         with torch.no_grad():
             _warm(torch, lambda: m4(q4, kv4, idx4), 3, 0.2)
             ms4 = _events_time(torch, lambda: m4(q4, kv4, idx4), max(5, a.steps // 5), stream)
-            c4_cold = cold(lambda: m4(q4, kv4, idx4), 5)
+            c4_cold = cold(lambda: m4(q4, kv4, idx4), 10)
         valid = int((idx4 >= 0).sum().item())
         flop4 = 4 * 64 * 128 * valid          # QK + PV over the valid slots
         b4 = t1_bytes(4, 4096, 64, 128, 8192, 512)
@@ -418,7 +453,7 @@ def main():
         with torch.no_grad():
             _warm(torch, lambda: m2(x, qr, sp, off), a.warmup, 0.2)
             ms2 = _events_time(torch, lambda: m2(x, qr, sp, off), a.steps, stream)
-            m2_cold = cold(lambda: m2(x, qr, sp, off), 10)
+            m2_cold = cold(lambda: m2(x, qr, sp, off), 20)
             # The kernels as Model.forward runs them: q projected and rotated by
             # dsa_indexer_q_proj, wl by F.linear, then the fused score / top-k kernel.
             fr = m2.freqs_cis[:2600]
@@ -430,7 +465,7 @@ def main():
             kfn = lambda: _native.indexer_score_topk(qp, m2.kv_cache, wl, scale, None, 32, 650, 128, 4, True, 0)
             _warm(torch, kfn, 3, 0.1)
             msk = _events_time(torch, kfn, a.steps, stream)
-            k_cold = cold(kfn, 10)
+            k_cold = cold(kfn, 20)
             _warm(torch, pfn, 3, 0.1)
             msp = _events_time(torch, pfn, a.steps, stream)
             # torch's projection for comparison (F.linear; RoPE then runs inside the score kernel)
