@@ -473,20 +473,33 @@ __global__ __launch_bounds__(64) void sa_mla_combine_kernel(MlaCombineParams p) 
   *reinterpret_cast<uint2*>(p.out + (tok * p.H + head) * kDV + 16 * ct + 4 * g) = pk;
 }
 
-// Split plan: with fewer tokens than CUs, each token's slot blocks are divided
-// among workgroups (at least DSA_MLA_MIN_BPS blocks each, at most kMaxSplit
-// splits) so up to about two workgroups per CU run.
-void mla_split_plan(int64_t tokens, int64_t topk, int cu, int* nsplit, int* bps) {
+// Split plan for few tokens (fewer than CUs): each token's heads go to hg head groups
+// (h / 16 / hg >= 2 waves each: one wave's copies of two blocks in flight would
+// exceed the vmcnt range) and its slot blocks to nsplit ranges (at least
+// DSA_MLA_MIN_BPS blocks each, at most kMaxSplit), one workgroup per (token, range,
+// group) and about one workgroup per CU in all (each holds the CU's LDS). More head
+// groups mean fewer waves per workgroup but fewer query bytes and partials per
+// workgroup; more ranges mean more partials to combine. Graph-replayed sweeps at
+// 128 heads, 2048 slots, 256 CUs put the best at 4 groups up to cu/64 tokens, 2 up to
+// cu/16, else 1, with nsplit = cu / (tokens * hg) (1-2 tokens: 32 x 4; 8: 16 x 2;
+// 16: 8 x 2; 32: 8 x 1; 64: 4 x 1; 128: 2 x 1; 192: one pass).
+void mla_split_plan(int64_t tokens, int64_t h, int64_t topk, int cu, int* nsplit, int* bps, int* hg) {
   const int nblk = (int)((topk + kKB - 1) / kKB);
   *nsplit = 1;
   *bps = nblk;
+  *hg = 1;
   if (tokens <= 0 || tokens >= cu || nblk < 2 * DSA_MLA_MIN_BPS) return;
-  int64_t want = (2 * (int64_t)cu + tokens - 1) / tokens;
+  int g = 1;
+  for (int c = 2; c <= 4; c *= 2)
+    if ((h / 16) % c == 0 && h / 16 / c >= 2 && tokens * 4 * c * c <= cu) g = c;
+  int64_t want = cu / (tokens * g);
   if (want > nblk / DSA_MLA_MIN_BPS) want = nblk / DSA_MLA_MIN_BPS;
   if (want > kMaxSplit) want = kMaxSplit;
+  if (want < 2) return;
   const int per = (int)((nblk + want - 1) / want);
   *bps = per;
   *nsplit = (nblk + per - 1) / per;
+  *hg = g;
 }
 
 int64_t mla_split_bytes(int64_t tokens, int64_t h, int nsplit) {
@@ -504,6 +517,8 @@ int mla_launch(const MlaParams& p, int nw, size_t smem, hipStream_t st) {
       return DSA_ERR_LAUNCH;                                                                      \
     hipLaunchKernelGGL((sa_mla_kernel<n, IdxT, kSplit>), grid, dim3(64 * n), smem, st, p);        \
     break;
+    DSA_MLA_CASE(2)
+    DSA_MLA_CASE(3)
     DSA_MLA_CASE(4)
     DSA_MLA_CASE(5)
     DSA_MLA_CASE(6)
@@ -557,8 +572,8 @@ int sparse_mla_fwd(const void* q, const void* kv, const void* topk_idxs, bool id
   if (workspace != nullptr) {
     int cu = 0;
     if (dsa_host::device_cu_count(&cu) != DSA_OK) return DSA_ERR_DEVICE;
-    int nsplit, bps;
-    mla_split_plan(b * m, topk, cu, &nsplit, &bps);
+    int nsplit, bps, hg;
+    mla_split_plan(b * m, h, topk, cu, &nsplit, &bps, &hg);
     const int64_t need = mla_split_bytes(b * m, h, nsplit);
     if (need > 0 && workspace_bytes >= need) {  // else the one-pass kernel (nothing to split)
       if (!dsa_host::aligned16(workspace)) return DSA_ERR_ALIGN;
@@ -567,10 +582,7 @@ int sparse_mla_fwd(const void* q, const void* kv, const void* topk_idxs, bool id
       p.ml = p.part + b * m * nsplit * h * kDV;
       p.nsplit = nsplit;
       p.bps = bps;
-      // Two head groups of 4 waves when 128 heads' workgroups would still leave most
-      // CUs idle: each workgroup then reads half the token's queries and writes half
-      // the partials, and twice as many CUs share the work.
-      if (h / 32 >= 4 && b * m * nsplit * 2 <= cu) p.hg = 2;
+      p.hg = hg;
     }
   }
   const size_t smem = (size_t)kRingM * kBlkBytes + (size_t)nblk * kKB * 4 + 32;  // + per-wave counts
@@ -618,8 +630,8 @@ extern "C" int64_t dsa_sparse_mla_workspace_bytes(int64_t b, int64_t m, int64_t 
   if (b == 0 || m == 0) return 0;
   int cu = 0;
   if (dsa_host::device_cu_count(&cu) != DSA_OK) return DSA_ERR_DEVICE;
-  int nsplit, bps;
-  mla_split_plan(b * m, topk, cu, &nsplit, &bps);
+  int nsplit, bps, hg;
+  mla_split_plan(b * m, h, topk, cu, &nsplit, &bps, &hg);
   return mla_split_bytes(b * m, h, nsplit);
 }
 

@@ -116,11 +116,13 @@ def test_mla_int64_indices_read_in_kernel(gpu):
 SPLIT_CASES = [
     # b, m, h, n_kv, topk, seed, masked, sink: few tokens, so the slot lists are split
     # over workgroups (dsa_sparse_mla_fwd_ws) and merged by the combine kernel
-    (1, 1, 128, 8192, 2048, 31, 0.0, 0.0),    # decode at the configs[4] size (2 head groups)
-    (1, 4, 128, 8192, 2048, 32, 0.1, 1.0),    # 4 x 32 ranges x 2 head groups: 256 workgroups
-    (1, 9, 128, 4000, 1024, 35, 0.05, 0.5),   # 9 x 16 ranges: 128 heads in one workgroup
-    (2, 16, 64, 3000, 300, 33, 0.3, -1.0),    # topk not a multiple of 32, 4 waves
-    (1, 3, 96, 700, 2000, 34, 0.0, 2.0),      # slots beyond n_kv (and beyond int32) masked
+    # (the plans are for 256 CUs: ranges x head groups per token)
+    (1, 1, 128, 8192, 2048, 31, 0.0, 0.0),    # decode at the configs[4] size: 32 x 4, 2 waves
+    (1, 4, 128, 8192, 2048, 32, 0.1, 1.0),    # 16 x 4: 256 workgroups
+    (1, 9, 128, 4000, 1024, 35, 0.05, 0.5),   # 11 x 2: 4 waves
+    (2, 16, 64, 3000, 300, 33, 0.3, -1.0),    # topk not a multiple of 32; 5 x 1, 4 waves
+    (1, 3, 96, 700, 2000, 34, 0.0, 2.0),      # slots beyond n_kv (and beyond int32) masked; 3 waves
+    (1, 2, 64, 5000, 1500, 36, 0.2, 0.0),     # 16 x 2: 64 heads as two 2-wave groups
 ]
 
 
