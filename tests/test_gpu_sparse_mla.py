@@ -123,6 +123,9 @@ SPLIT_CASES = [
     (2, 16, 64, 3000, 300, 33, 0.3, -1.0),    # topk not a multiple of 32; 5 x 1, 4 waves
     (1, 3, 96, 700, 2000, 34, 0.0, 2.0),      # slots beyond n_kv (and beyond int32) masked; 3 waves
     (1, 2, 64, 5000, 1500, 36, 0.2, 0.0),     # 16 x 2: 64 heads as two 2-wave groups
+    (1, 17, 128, 3000, 1024, 37, 0.1, 0.0),   # 11 x 1: 8 waves
+    (1, 40, 128, 2000, 512, 38, 0.0, 0.5),    # 6 x 1
+    (2, 50, 64, 4000, 2048, 39, 0.05, 0.0),   # 100 tokens: 2 x 1
 ]
 
 
