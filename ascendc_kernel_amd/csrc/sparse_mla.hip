@@ -81,7 +81,10 @@ void sa_mla_kernel(MlaParams p) {
   // head group hgi.
   const int hgi = kSplit ? (int)(blockIdx.x % p.hg) : 0;
   const int64_t tsp = kSplit ? (int64_t)(blockIdx.x / p.hg) : 0;
-  const int64_t tok = kSplit ? tsp / p.nsplit : (int64_t)blockIdx.x;
+  // One-pass mode takes the tokens last to first: with causal slot lists the late
+  // tokens have the most blocks, so the short early tokens fill the end of the grid
+  // (2-3 % at configs[4]).
+  const int64_t tok = kSplit ? tsp / p.nsplit : (int64_t)(gridDim.x - 1 - blockIdx.x);
   const int sp = kSplit ? (int)(tsp % p.nsplit) : 0;
   const int kb0 = kSplit ? sp * p.bps : 0;
   const int nbl = kSplit ? max(0, min(p.bps, nblk - kb0)) : nblk;
