@@ -14,7 +14,7 @@ import torch
 
 from . import build as _build
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DSA_SA_AUTO = 0
 DSA_SA_MULTIPLICITY = 1
@@ -40,6 +40,8 @@ EXPORTS = (
     "dsa_indexer_score_topk_noalloc",
     "dsa_indexer_scores",
     "dsa_indexer_q_proj",
+    "dsa_indexer_pack_projection_weights",
+    "dsa_indexer_projections",
 )
 
 _c_i64 = ctypes.c_int64
@@ -124,6 +126,13 @@ def load() -> ctypes.CDLL:
     lib.dsa_indexer_q_proj.restype = ctypes.c_int
     lib.dsa_indexer_q_proj.argtypes = [
         _c_vp, _c_vp, _c_vp, ctypes.c_int32, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]
+    lib.dsa_indexer_pack_projection_weights.restype = ctypes.c_int
+    lib.dsa_indexer_pack_projection_weights.argtypes = [
+        _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp]
+    lib.dsa_indexer_projections.restype = ctypes.c_int
+    lib.dsa_indexer_projections.argtypes = [
+        _c_vp, _c_vp, _c_vp, ctypes.c_int32, _c_vp, _c_vp, _c_vp, _c_vp,
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]
     v = lib.dsa_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {v}, expected {ABI_VERSION}")
@@ -141,6 +150,37 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+#: device type whose calls the modules serve from a cached launch plan (tests of the plan
+#: logic on the CPU switch it)
+PLAN_DEVICE_TYPE = "cuda"
+
+
+def stream_handle(dev: torch.device) -> int:
+    """hipStream_t of the current stream on `dev` as an int (the cheap query when torch has it)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+class Launch:
+    """One prepared C-ABI call: the resolved entry point and its marshalled arguments, with
+    the slots that change per call (fresh outputs) patched by index. Built on the first call
+    with a given set of pointers and shapes; later calls skip the checks and the marshalling."""
+    __slots__ = ("name", "fn", "args")
+
+    def __init__(self, name: str, args: list):
+        self.name = name
+        self.fn = getattr(load(), name)
+        self.args = args
+
+    def __call__(self) -> None:
+        rc = self.fn(*self.args)
+        if rc != 0:
+            _check(self.name, rc)
+
+
 def _require_gpu(*ts: torch.Tensor) -> torch.device:
     dev = ts[0].device
     for t in ts:
@@ -152,11 +192,32 @@ def _require_gpu(*ts: torch.Tensor) -> torch.device:
     return dev
 
 
-def sparse_attn_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
-                    attn_sink: torch.Tensor, softmax_scale: float,
-                    variant: int = DSA_SA_AUTO) -> torch.Tensor:
-    """Task1 forward on the GPU; shapes as in reference/task1_v0_ref.py:5-24."""
-    lib = load()
+class Prepared:
+    """A checked, marshalled call and what it needs kept alive (inputs made contiguous,
+    workspaces, the fp32 sink copy). run() allocates the fresh output, patches its pointer
+    into the argument slot `out_slot` and launches."""
+    __slots__ = ("launch", "out_slot", "out_shape", "out_dtype", "device", "keep")
+
+    def __init__(self, launch: Launch, out_slot: int, out_shape, out_dtype, device, keep):
+        self.launch = launch
+        self.out_slot = out_slot
+        self.out_shape = out_shape
+        self.out_dtype = out_dtype
+        self.device = device
+        self.keep = keep
+
+    def run(self) -> torch.Tensor:
+        out = torch.empty(self.out_shape, dtype=self.out_dtype, device=self.device)
+        self.launch.args[self.out_slot] = out.data_ptr()
+        self.launch()
+        return out
+
+
+def prepare_sparse_attn(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
+                        attn_sink: torch.Tensor, softmax_scale: float,
+                        variant: int = DSA_SA_AUTO) -> Prepared:
+    """Checks and marshals dsa_sparse_attn_fwd[_i64] (output slot 4)."""
+    load()
     if q.dim() != 4 or kv.dim() != 3 or topk_idxs.dim() != 3:
         raise ValueError("expected q [b,m,h,d], kv [b,n_kv,d], topk_idxs [b,m,topk]")
     b, m, h, d = q.shape
@@ -175,20 +236,23 @@ def sparse_attn_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
     idx = topk_idxs.contiguous()  # int64 indices are read as they are (no narrowing pass)
     fn = "dsa_sparse_attn_fwd_i64" if idx.dtype == torch.int64 else "dsa_sparse_attn_fwd"
     sink = attn_sink.detach().to(device=dev, dtype=torch.float32).contiguous()
-    out = torch.empty_like(q)
-    rc = getattr(lib, fn)(
-        q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), out.data_ptr(),
-        b, m, h, d, kv.shape[1], idx.shape[2], float(softmax_scale), int(variant), _stream(q))
-    _check(fn, rc)
-    return out
+    args = [q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), None,
+            b, m, h, d, kv.shape[1], idx.shape[2], float(softmax_scale), int(variant), stream_handle(dev)]
+    return Prepared(Launch(fn, args), 4, (b, m, h, d), torch.bfloat16, dev, (q, kv, idx, sink))
 
 
-def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
-                   attn_sink: torch.Tensor, softmax_scale: float, v_dim: int,
-                   split: bool = True) -> torch.Tensor:
-    """Sparse MLA on the GPU: q [b,m,h,d_qk], kv [b,n_kv,>=d_qk]; keys are kv[..., :d_qk],
-    values kv[..., :v_dim]; returns bf16 [b,m,h,v_dim]. split=False keeps the one-pass
-    kernel also where the library would split the slot lists (few tokens)."""
+def sparse_attn_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
+                    attn_sink: torch.Tensor, softmax_scale: float,
+                    variant: int = DSA_SA_AUTO) -> torch.Tensor:
+    """Task1 forward on the GPU; shapes as in reference/task1_v0_ref.py:5-24."""
+    return prepare_sparse_attn(q, kv, topk_idxs, attn_sink, softmax_scale, variant).run()
+
+
+def prepare_sparse_mla(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
+                       attn_sink: torch.Tensor, softmax_scale: float, v_dim: int,
+                       split: bool = True) -> Prepared:
+    """Checks and marshals dsa_sparse_mla_fwd[_i64][_ws] (output slot 4); the workspace of
+    a split launch is allocated here and reused by every run() (calls on one stream)."""
     lib = load()
     if q.dim() != 4 or kv.dim() != 3 or topk_idxs.dim() != 3:
         raise ValueError("expected q [b,m,h,d_qk], kv [b,n_kv,kv_dim], topk_idxs [b,m,topk]")
@@ -207,23 +271,32 @@ def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
     kv = kv.contiguous()
     idx = topk_idxs.contiguous()  # int64 indices are read as they are (no narrowing pass)
     sink = attn_sink.detach().to(device=dev, dtype=torch.float32).contiguous()
-    out = torch.empty(b, m, h, v_dim, dtype=torch.bfloat16, device=dev)
-    args = (q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), out.data_ptr(),
-            b, m, h, dqk, v_dim, kv.shape[2], kv.shape[1], idx.shape[2], float(softmax_scale))
+    args = [q.data_ptr(), kv.data_ptr(), idx.data_ptr(), sink.data_ptr(), None,
+            b, m, h, dqk, v_dim, kv.shape[2], kv.shape[1], idx.shape[2], float(softmax_scale)]
     # Few tokens (decode): the slot lists are split over workgroups whose partial
     # results go to a workspace from torch's caching allocator.
     ws_bytes = int(lib.dsa_sparse_mla_workspace_bytes(b, m, h, idx.shape[2])) if split else 0
     if ws_bytes < 0:
         _check("dsa_sparse_mla_workspace_bytes", ws_bytes)
+    keep = [q, kv, idx, sink]
     if ws_bytes > 0:
         fn = "dsa_sparse_mla_fwd_i64_ws" if idx.dtype == torch.int64 else "dsa_sparse_mla_fwd_ws"
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        rc = getattr(lib, fn)(*args, ws.data_ptr(), ws_bytes, _stream(q))
+        keep.append(ws)
+        args += [ws.data_ptr(), ws_bytes]
     else:
         fn = "dsa_sparse_mla_fwd_i64" if idx.dtype == torch.int64 else "dsa_sparse_mla_fwd"
-        rc = getattr(lib, fn)(*args, _stream(q))
-    _check(fn, rc)
-    return out
+    args.append(stream_handle(dev))
+    return Prepared(Launch(fn, args), 4, (b, m, h, v_dim), torch.bfloat16, dev, tuple(keep))
+
+
+def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor,
+                   attn_sink: torch.Tensor, softmax_scale: float, v_dim: int,
+                   split: bool = True) -> torch.Tensor:
+    """Sparse MLA on the GPU: q [b,m,h,d_qk], kv [b,n_kv,>=d_qk]; keys are kv[..., :d_qk],
+    values kv[..., :v_dim]; returns bf16 [b,m,h,v_dim]. split=False keeps the one-pass
+    kernel also where the library would split the slot lists (few tokens)."""
+    return prepare_sparse_mla(q, kv, topk_idxs, attn_sink, softmax_scale, v_dim, split).run()
 
 
 def indexer_rope_(q: torch.Tensor, freqs_cis: torch.Tensor, rope_head_dim: int,
@@ -250,17 +323,17 @@ def _freqs_view(freqs_cis: torch.Tensor, s: int, rd: int) -> torch.Tensor:
     return torch.view_as_real(fr[:s].contiguous())
 
 
-def indexer_score_topk(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor,
-                       w_scale: float, freqs_cis: Optional[torch.Tensor], rope_head_dim: int,
-                       n_cand: int, k_out: int, ratio: int, causal: bool, offset: int,
-                       rope_mode: int = DSA_ROPE_TORCH_ROCM, use_workspace: bool = True) -> torch.Tensor:
-    """Task2 score + mask + top-k; returns int64 [b, s, k_out].
+#: argument slots of dsa_indexer_score_topk[_ws] that change per call
+SCORE_SLOT_Q, SCORE_SLOT_WL, SCORE_SLOT_OUT = 0, 3, 7
 
-    q: bf16 [b, s, h, d] (contiguous); kv_cache: bf16 [>=b, >=n_cand, d] with unit
-    row stride; wl: bf16 [b, s, h]; freqs_cis: complex64 rows for the s positions.
-    When the configuration takes a workspace (64 heads x 128) it is allocated from
-    torch's caching allocator and passed in (use_workspace=False: the single-kernel path).
-    """
+
+def prepare_indexer_score_topk(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor,
+                               w_scale: float, freqs_cis: Optional[torch.Tensor], rope_head_dim: int,
+                               n_cand: int, k_out: int, ratio: int, causal: bool, offset: int,
+                               rope_mode: int = DSA_ROPE_TORCH_ROCM,
+                               use_workspace: bool = True) -> Prepared:
+    """Checks and marshals dsa_indexer_score_topk[_ws]: q, wl and out in the argument slots
+    SCORE_SLOT_*; a workspace is allocated here and reused by every run()."""
     lib = load()
     b, s, h, d = q.shape
     if q.dtype != torch.bfloat16 or kv_cache.dtype != torch.bfloat16 or wl.dtype != torch.bfloat16:
@@ -274,27 +347,38 @@ def indexer_score_topk(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor
     q = q.contiguous()
     wl = wl.contiguous()
     fr = _freqs_view(freqs_cis, s, rope_head_dim) if freqs_cis is not None else None
-    _require_gpu(q, kv_cache, wl, *([fr] if fr is not None else []))
-    out = torch.empty(b, s, k_out, dtype=torch.int64, device=q.device)
+    dev = _require_gpu(q, kv_cache, wl, *([fr] if fr is not None else []))
+    args = [q.data_ptr(), kv_cache.data_ptr(), kv_cache.stride(0), wl.data_ptr(), float(w_scale),
+            fr.data_ptr() if fr is not None else None, int(rope_mode), None,
+            b, s, h, d, rope_head_dim, n_cand, k_out, ratio, 1 if causal else 0, int(offset)]
     ws_bytes = int(lib.dsa_indexer_workspace_bytes(b, s, h, d, n_cand)) if use_workspace else 0
     if ws_bytes < 0:
         _check("dsa_indexer_workspace_bytes", ws_bytes)
+    keep = [q, kv_cache, wl, fr]
     if ws_bytes > 0:
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-        rc = lib.dsa_indexer_score_topk_ws(
-            q.data_ptr(), kv_cache.data_ptr(), kv_cache.stride(0), wl.data_ptr(), float(w_scale),
-            fr.data_ptr() if fr is not None else None, int(rope_mode), out.data_ptr(),
-            b, s, h, d, rope_head_dim, n_cand, k_out, ratio, 1 if causal else 0, int(offset),
-            ws.data_ptr(), ws_bytes, _stream(q))
-        _check("dsa_indexer_score_topk_ws", rc)
-        return out
-    rc = lib.dsa_indexer_score_topk(
-        q.data_ptr(), kv_cache.data_ptr(), kv_cache.stride(0), wl.data_ptr(), float(w_scale),
-        fr.data_ptr() if fr is not None else None, int(rope_mode), out.data_ptr(),
-        b, s, h, d, rope_head_dim, n_cand, k_out, ratio, 1 if causal else 0, int(offset),
-        _stream(q))
-    _check("dsa_indexer_score_topk", rc)
-    return out
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        keep.append(ws)
+        fn = "dsa_indexer_score_topk_ws"
+        args += [ws.data_ptr(), ws_bytes]
+    else:
+        fn = "dsa_indexer_score_topk"
+    args.append(stream_handle(dev))
+    return Prepared(Launch(fn, args), SCORE_SLOT_OUT, (b, s, k_out), torch.int64, dev, tuple(keep))
+
+
+def indexer_score_topk(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor,
+                       w_scale: float, freqs_cis: Optional[torch.Tensor], rope_head_dim: int,
+                       n_cand: int, k_out: int, ratio: int, causal: bool, offset: int,
+                       rope_mode: int = DSA_ROPE_TORCH_ROCM, use_workspace: bool = True) -> torch.Tensor:
+    """Task2 score + mask + top-k; returns int64 [b, s, k_out].
+
+    q: bf16 [b, s, h, d] (contiguous); kv_cache: bf16 [>=b, >=n_cand, d] with unit
+    row stride; wl: bf16 [b, s, h]; freqs_cis: complex64 rows for the s positions.
+    When the configuration takes a workspace (64 heads x 128) it is allocated from
+    torch's caching allocator and passed in (use_workspace=False: the single-kernel path).
+    """
+    return prepare_indexer_score_topk(q, kv_cache, wl, w_scale, freqs_cis, rope_head_dim, n_cand, k_out,
+                                      ratio, causal, offset, rope_mode, use_workspace).run()
 
 
 def indexer_scores(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor, w_scale: float,
@@ -318,13 +402,11 @@ def indexer_scores(q: torch.Tensor, kv_cache: torch.Tensor, wl: torch.Tensor, w_
     return out
 
 
-def indexer_q_proj(qr: torch.Tensor, weight: torch.Tensor, freqs_cis: Optional[torch.Tensor],
-                   head_dim: int, rope_head_dim: int,
-                   rope_mode: int = DSA_ROPE_TORCH_ROCM) -> torch.Tensor:
-    """q = qr . weight^T as bf16 [b, s, n/head_dim, head_dim] (F.linear's rounding), with
-    RoPE on the last rope_head_dim channels of every head when freqs_cis (rows for the s
-    positions) is given. qr: bf16 [b, s, k]; weight: bf16 [n, k]."""
-    lib = load()
+def prepare_indexer_q_proj(qr: torch.Tensor, weight: torch.Tensor, freqs_cis: Optional[torch.Tensor],
+                           head_dim: int, rope_head_dim: int,
+                           rope_mode: int = DSA_ROPE_TORCH_ROCM) -> Prepared:
+    """Checks and marshals dsa_indexer_q_proj (output q in slot 4)."""
+    load()
     if qr.dim() != 3 or weight.dim() != 2 or qr.shape[2] != weight.shape[1]:
         raise ValueError(f"qr {tuple(qr.shape)} and weight {tuple(weight.shape)} do not match")
     if qr.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
@@ -332,12 +414,93 @@ def indexer_q_proj(qr: torch.Tensor, weight: torch.Tensor, freqs_cis: Optional[t
     b, s, k = qr.shape
     n = weight.shape[0]
     qr = qr.contiguous()
-    weight = weight.contiguous()
+    weight = weight.detach().contiguous()
     fr = _freqs_view(freqs_cis, s, rope_head_dim) if freqs_cis is not None else None
-    _require_gpu(qr, weight, *([fr] if fr is not None else []))
-    out = torch.empty(b, s, n // head_dim, head_dim, dtype=torch.bfloat16, device=qr.device)
-    rc = lib.dsa_indexer_q_proj(qr.data_ptr(), weight.data_ptr(), fr.data_ptr() if fr is not None else None,
-                                int(rope_mode), out.data_ptr(), b * s, n, k, head_dim, rope_head_dim,
-                                max(s, 1), _stream(qr))
-    _check("dsa_indexer_q_proj", rc)
-    return out
+    dev = _require_gpu(qr, weight, *([fr] if fr is not None else []))
+    args = [qr.data_ptr(), weight.data_ptr(), fr.data_ptr() if fr is not None else None, int(rope_mode), None,
+            b * s, n, k, head_dim, rope_head_dim, max(s, 1), stream_handle(dev)]
+    return Prepared(Launch("dsa_indexer_q_proj", args), 4, (b, s, n // head_dim, head_dim), torch.bfloat16,
+                    dev, (qr, weight, fr))
+
+
+def indexer_q_proj(qr: torch.Tensor, weight: torch.Tensor, freqs_cis: Optional[torch.Tensor],
+                   head_dim: int, rope_head_dim: int,
+                   rope_mode: int = DSA_ROPE_TORCH_ROCM) -> torch.Tensor:
+    """q = qr . weight^T as bf16 [b, s, n/head_dim, head_dim] (F.linear's rounding), with
+    RoPE on the last rope_head_dim channels of every head when freqs_cis (rows for the s
+    positions) is given. qr: bf16 [b, s, k]; weight: bf16 [n, k]."""
+    return prepare_indexer_q_proj(qr, weight, freqs_cis, head_dim, rope_head_dim, rope_mode).run()
+
+
+def pack_projection_weights(wq: Optional[torch.Tensor], wproj: Optional[torch.Tensor]):
+    """Fragment-packed copies of the indexer's projection weights for
+    ``indexer_projections``: wq bf16 [n, 256] and wproj bf16 [n_w, dim] (either may be
+    None). A permutation of the same bytes; pack once per weight version."""
+    lib = load()
+    ts = [t for t in (wq, wproj) if t is not None]
+    if not ts:
+        return None, None
+    dev = _require_gpu(*ts)
+    for t in ts:
+        if t.dim() != 2 or t.dtype != torch.bfloat16:
+            raise TypeError("projection weights must be 2-D bfloat16 tensors")
+    wq_c = wq.detach().contiguous() if wq is not None else None
+    wp_c = wproj.detach().contiguous() if wproj is not None else None
+    wq_p = torch.empty_like(wq_c) if wq_c is not None else None
+    wp_p = torch.empty_like(wp_c) if wp_c is not None else None
+    rc = lib.dsa_indexer_pack_projection_weights(
+        wq_c.data_ptr() if wq_c is not None else None,
+        wq_c.shape[0] if wq_c is not None else 0, wq_c.shape[1] if wq_c is not None else 0,
+        wp_c.data_ptr() if wp_c is not None else None,
+        wp_c.shape[0] if wp_c is not None else 0, wp_c.shape[1] if wp_c is not None else 0,
+        wq_p.data_ptr() if wq_p is not None else None, wp_p.data_ptr() if wp_p is not None else None,
+        stream_handle(dev))
+    _check("dsa_indexer_pack_projection_weights", rc)
+    return wq_p, wp_p
+
+
+#: argument slots of dsa_indexer_projections holding the outputs q and wl
+PROJ_SLOT_Q, PROJ_SLOT_WL = 4, 7
+
+
+def prepare_indexer_projections(qr: torch.Tensor, wq_packed: torch.Tensor, freqs_cis: Optional[torch.Tensor],
+                                x: torch.Tensor, wproj_packed: torch.Tensor, head_dim: int, rope_head_dim: int,
+                                rope_mode: int = DSA_ROPE_TORCH_ROCM):
+    """Checks and marshals dsa_indexer_projections; returns (Launch, q_shape, wl_shape, keep)
+    with the outputs in the argument slots PROJ_SLOT_Q and PROJ_SLOT_WL."""
+    load()
+    if qr.dim() != 3 or x.dim() != 3 or qr.shape[:2] != x.shape[:2]:
+        raise ValueError(f"qr {tuple(qr.shape)} and x {tuple(x.shape)} do not match")
+    if qr.dtype != torch.bfloat16 or x.dtype != torch.bfloat16:
+        raise TypeError("qr and x must be bfloat16")
+    b, s, k = qr.shape
+    dim = x.shape[2]
+    n = wq_packed.shape[0]
+    n_w = wproj_packed.shape[0]
+    if wq_packed.shape[1] != k or wproj_packed.shape[1] != dim:
+        raise ValueError("packed weights do not match qr / x")
+    qr = qr.contiguous()
+    x = x.contiguous()
+    fr = _freqs_view(freqs_cis, s, rope_head_dim) if freqs_cis is not None else None
+    dev = _require_gpu(qr, x, wq_packed, wproj_packed, *([fr] if fr is not None else []))
+    args = [qr.data_ptr(), wq_packed.data_ptr(), fr.data_ptr() if fr is not None else None, int(rope_mode),
+            None, x.data_ptr(), wproj_packed.data_ptr(), None,
+            b * s, n, k, dim, n_w, head_dim, rope_head_dim, max(s, 1), stream_handle(dev)]
+    return (Launch("dsa_indexer_projections", args), (b, s, n // head_dim, head_dim), (b, s, n_w),
+            (qr, x, wq_packed, wproj_packed, fr))
+
+
+def indexer_projections(qr: torch.Tensor, wq_packed: torch.Tensor, freqs_cis: Optional[torch.Tensor],
+                        x: torch.Tensor, wproj_packed: torch.Tensor, head_dim: int, rope_head_dim: int,
+                        rope_mode: int = DSA_ROPE_TORCH_ROCM):
+    """Both indexer projections in one launch: q = RoPE(qr . wq^T) as bf16
+    [b, s, n/head_dim, head_dim] and wl = x . wproj^T as bf16 [b, s, n_w], from the
+    packed weights of ``pack_projection_weights``. qr: bf16 [b, s, 256]; x: bf16 [b, s, dim]."""
+    launch, q_shape, wl_shape, _keep = prepare_indexer_projections(qr, wq_packed, freqs_cis, x, wproj_packed,
+                                                                   head_dim, rope_head_dim, rope_mode)
+    q = torch.empty(q_shape, dtype=torch.bfloat16, device=qr.device)
+    wl = torch.empty(wl_shape, dtype=torch.bfloat16, device=qr.device)
+    launch.args[PROJ_SLOT_Q] = q.data_ptr()
+    launch.args[PROJ_SLOT_WL] = wl.data_ptr()
+    launch()
+    return q, wl

@@ -33,16 +33,36 @@ class Model(nn.Module):
         self.v_dim = v_dim
         self.softmax_scale = head_dim ** -0.5
         self.attn_sink = nn.Parameter(torch.zeros(n_heads, dtype=torch.float32))
+        # (key, _native.Prepared) of the last call. The prepared launch holds its inputs, so
+        # their memory cannot be reused for other tensors (which could repeat a pointer)
+        # while the key that names them is cached.
+        self._plan = None
 
     def forward(self, q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor) -> torch.Tensor:
-        if q.shape[2] != self.n_heads or q.shape[3] != self.head_dim:
+        # Steady state (the Ascend ModelNew's fast path binds its launch after the third call
+        # with the same input pointers, src/task1_sparse_attn.py:751-755,789-801): the same
+        # pointers, shapes, dtypes, sink and stream as the last call reuse its checked and
+        # marshalled launch; only the fresh output is allocated. Anything else (including an
+        # in-place update of attn_sink, which moves its version counter) prepares anew.
+        dev = q.device
+        if dev.type == _native.PLAN_DEVICE_TYPE and q.is_contiguous() and kv.is_contiguous() and topk_idxs.is_contiguous():
+            sink = self.attn_sink
+            key = (q.data_ptr(), kv.data_ptr(), topk_idxs.data_ptr(), q.shape, kv.shape, topk_idxs.shape,
+                   q.dtype, kv.dtype, topk_idxs.dtype, sink.data_ptr(), sink._version,
+                   _native.stream_handle(dev), self.variant, self.v_dim)
+            plan = self._plan
+            if plan is None or plan[0] != key:
+                plan = self._plan = (key, self._prepare(q, kv, topk_idxs))
+            return plan[1].run()
+        return self._prepare(q, kv, topk_idxs).run()
+
+    def _prepare(self, q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor) -> "_native.Prepared":
+        if q.dim() != 4 or q.shape[2] != self.n_heads or q.shape[3] != self.head_dim:
             raise ValueError(f"q {tuple(q.shape)} does not match n_heads={self.n_heads}, "
                              f"head_dim={self.head_dim}")
         if self.v_dim is not None and self.v_dim != self.head_dim:
-            return _native.sparse_mla_fwd(q, kv, topk_idxs, self.attn_sink, self.softmax_scale,
-                                          self.v_dim)
-        return _native.sparse_attn_fwd(q, kv, topk_idxs, self.attn_sink, self.softmax_scale,
-                                       self.variant)
+            return _native.prepare_sparse_mla(q, kv, topk_idxs, self.attn_sink, self.softmax_scale, self.v_dim)
+        return _native.prepare_sparse_attn(q, kv, topk_idxs, self.attn_sink, self.softmax_scale, self.variant)
 
 
 # The Ascend submission names its module ModelNew (src/task1_sparse_attn.py:666).

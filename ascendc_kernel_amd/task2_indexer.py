@@ -8,13 +8,18 @@ Same surface as reference/task2_v0_ref.py: ``ModelArgs`` (:21-61), the
 constructor creates ``wq_b`` then ``weights_proj`` with the same initialisers,
 so a seeded construction yields the reference's weights.
 
-forward = two torch projections (``F.linear``, the reference's own op) and one
-gfx950 kernel that applies RoPE, the score, the relu-weighted head sum, the
-causal mask and the top-k (``dsa_indexer_score_topk``). Inputs must be on the
-HIP device; unsupported configurations raise.
+forward = the two projections, then one gfx950 kernel for the score, the
+relu-weighted head sum, the causal mask and the top-k (``dsa_indexer_score_topk``).
+The projections run as one kernel launch (``dsa_indexer_projections``: q with RoPE,
+and the head weights), as the query-projection kernel beside ``F.linear``, or as two
+``F.linear`` (the reference's own op; the score kernel then applies RoPE), whichever
+``projection_route`` picks: a kernel only where its rounding was measured equal to
+``F.linear`` on this torch-ROCm build. Inputs must be on the HIP device;
+unsupported configurations raise.
 """
 from __future__ import annotations
 
+import bisect
 import math
 from dataclasses import dataclass
 from typing import Literal, Tuple
@@ -107,6 +112,74 @@ class ColumnParallelLinear(Linear):
         super().__init__(in_features, self.part_out_features, bias, dtype)
 
 
+#: The torch-ROCm build (torch.__version__, torch.version.hip) and CU count on which the
+#: projection kernels' rounding was measured against F.linear (hipBLASLt chooses its
+#: algorithm, and with it the order in which it sums k, by build, shape and CU count); on
+#: anything else Model.forward keeps F.linear.
+MEASURED_TORCH = ("2.10.0+rocm7.0", "7.0.51831")
+MEASURED_CUS = 256
+#: Token counts m = b * s (maximal intervals, inclusive) where F.linear equals the kernels'
+#: natural-order k accumulation bit for bit on that build, measured for every m from 17 to
+#: 131,072 by tests/golden/measure_projection_ranges.py (tests/golden/projection_ranges.json):
+#: wq_b (k = 256, 1024 outputs) and weights_proj (k = 1024, 16 outputs). Between the
+#: intervals hipBLASLt splits the k sum (over wave groups, or stream-K tails).
+Q_EQUAL = (
+    (17, 32768), (33153, 34304), (34433, 35456), (35585, 36608), (36737, 52096), (52225, 65664),
+    (65793, 65920), (66433, 67584), (67713, 68736), (68865, 69888), (70017, 71040), (71169, 73344),
+    (73473, 81920), (82049, 82176), (82433, 82560), (82817, 83328), (83457, 83712), (83841, 86144),
+    (86273, 86528), (86657, 87552), (87681, 87936), (88065, 98304), (98433, 98560), (99329, 100608),
+    (100737, 100992), (101121, 101888), (102017, 102272), (102401, 102656), (102785, 103936),
+    (104065, 104320), (104449, 105216), (105345, 105984), (106113, 114688), (115073, 115200),
+    (115585, 115712), (115841, 117504), (117633, 118016), (118145, 118528), (118657, 119040),
+    (119169, 119424), (119553, 119936), (120065, 120448), (120577, 120960), (121089, 121344),
+    (121473, 121856), (121985, 122368), (122497, 131072),
+)
+WL_EQUAL = (
+    (17, 140), (15361, 15517), (15617, 15772), (15873, 16026), (16129, 16281), (16385, 65536),
+    (65793, 66048), (66305, 66560), (66817, 67072), (67329, 67584), (67841, 68096), (68353, 68608),
+    (68865, 69120), (69377, 69632), (69889, 70144), (70401, 70656), (70913, 71168), (71425, 71680),
+    (71937, 72192), (72449, 72704), (72961, 73216), (73473, 73728), (73985, 74240), (74497, 74752),
+    (75009, 75264), (75521, 75776), (76033, 76288), (76545, 76800), (77057, 77824), (78081, 78336),
+    (78593, 131072),
+)
+#: smallest token count sent to the query-projection kernel (below it F.linear + the score
+#: kernel's own RoPE is as fast)
+Q_PROJ_MIN_TOKENS = 64
+
+_build_ok: dict = {}
+
+
+def _measured_build(dev: torch.device) -> bool:
+    ok = _build_ok.get(dev.index)
+    if ok is None:
+        ok = ((torch.__version__, torch.version.hip) == MEASURED_TORCH
+              and torch.cuda.get_device_properties(dev).multi_processor_count == MEASURED_CUS)
+        _build_ok[dev.index] = ok
+    return ok
+
+
+def _within(m: int, table) -> bool:
+    i = bisect.bisect_right(table, (m, float("inf"))) - 1
+    return i >= 0 and table[i][0] <= m <= table[i][1]
+
+
+def projection_route(m: int, q_lora_rank: int, rope_head_dim: int, head_dim: int, n_q: int, dim: int,
+                     n_w: int, bf16: bool, on_gpu: bool, build_ok: bool) -> str:
+    """Which path computes the two projections of Model.forward for m = b * s tokens:
+    'both'  one launch of dsa_indexer_projections (q with RoPE, and weights_proj);
+    'q'     dsa_indexer_q_proj for q with RoPE, F.linear for weights_proj;
+    'torch' F.linear for both (the score kernel then applies RoPE).
+    A kernel is used only where its rounding was measured equal to F.linear."""
+    if not (bf16 and on_gpu and build_ok):
+        return "torch"
+    if not (q_lora_rank == 256 and rope_head_dim == 32 and n_q % 256 == 0 and head_dim in (64, 128)
+            and m >= Q_PROJ_MIN_TOKENS and _within(m, Q_EQUAL)):
+        return "torch"
+    if head_dim == 64 and dim == 1024 and n_w == 16 and _within(m, WL_EQUAL):
+        return "both"
+    return "q"
+
+
 class Model(nn.Module):
     """Drop-in for ``Model`` of reference/task2_v0_ref.py:106-144."""
 
@@ -129,44 +202,138 @@ class Model(nn.Module):
         self.compress_ratio = compress_ratio
         self.kv_cache = kv_cache
         self.freqs_cis = freqs_cis
+        # The last call's launch plan, and the fragment-packed projection weights with the
+        # (pointer, version) pairs they were packed from. Plans hold their inputs, so their
+        # memory cannot be reused for other tensors (which could repeat a pointer) while the
+        # key that names them is cached.
+        self._plan = None
+        self._packed = None
+
+    def route(self, x: torch.Tensor, qr: torch.Tensor) -> str:
+        """projection_route for these inputs ('both', 'q' or 'torch')."""
+        wq, wp = self.wq_b.weight, self.weights_proj.weight
+        return projection_route(
+            qr.shape[0] * qr.shape[1], qr.shape[-1], self.rope_head_dim, self.head_dim, wq.shape[0], x.shape[-1],
+            wp.shape[0], qr.dtype == x.dtype == wq.dtype == wp.dtype == torch.bfloat16,
+            qr.is_cuda and x.is_cuda, qr.is_cuda and _measured_build(qr.device))
 
     def forward(self, x: torch.Tensor, qr: torch.Tensor, start_pos: int, offset: int) -> torch.Tensor:
-        bsz, seqlen, _ = x.size()
-        ratio = self.compress_ratio
-        end_pos = start_pos + seqlen
-        n_cand = end_pos // ratio
-        k_out = min(self.index_topk, n_cand)
-        if k_out <= 0:
-            return torch.empty(bsz, seqlen, 0, dtype=torch.int64, device=x.device)
-        freqs = self.freqs_cis[start_pos:end_pos]
-        if self._q_proj_fused(qr):
-            # q = RoPE(qr . wq_b^T) in one kernel, bit-equal to F.linear + apply_rotary_emb
-            # (task2_v0_ref.py:129-131) for this shape class.
-            q = _native.indexer_q_proj(qr, self.wq_b.weight, freqs, self.head_dim, self.rope_head_dim,
-                                       self.rope_mode)
-            freqs = None
-        else:
-            q = self.wq_b(qr).unflatten(-1, (self.n_local_heads, self.head_dim))
-        wl = self.weights_proj(x)
-        w_scale = self.softmax_scale * self.n_heads ** -0.5
-        return _native.indexer_score_topk(
-            q, self.kv_cache, wl, w_scale, freqs, self.rope_head_dim,
-            n_cand, k_out, ratio, start_pos == 0, offset, self.rope_mode)
+        # Steady state (the Ascend ModelNew binds a no-argument launch of the whole forward
+        # after the third call with the same pointers, src/task2_indexer.py:1069-1072,
+        # 1340-1348): the same inputs, positions, weights (pointer and version), cache, table
+        # and stream as the last call reuse its plan; only the fresh output is allocated.
+        dev = x.device
+        wq, wp, kv, fc = self.wq_b.weight, self.weights_proj.weight, self.kv_cache, self.freqs_cis
+        # (A plan reads kv_cache and freqs_cis in place, so it sees their updates; it is kept
+        # only where neither needs a contiguous copy, which would not.)
+        if (dev.type == _native.PLAN_DEVICE_TYPE and x.is_contiguous() and qr.is_contiguous() and kv.dim() == 3
+                and kv.stride(2) == 1 and kv.stride(1) == kv.shape[2] and fc.is_contiguous()):
+            key = (x.data_ptr(), qr.data_ptr(), x.shape, qr.shape, x.dtype, qr.dtype, start_pos, offset,
+                   wq.data_ptr(), wq._version, wp.data_ptr(), wp._version, kv.data_ptr(), kv.shape,
+                   kv.stride(), fc.data_ptr(), fc.shape, _native.stream_handle(dev), self.rope_mode,
+                   self.compress_ratio, self.index_topk)
+            plan = self._plan
+            if plan is None or plan.key != key:
+                plan = self._plan = _IndexerPlan(self, x, qr, start_pos, offset, key)
+            return plan.run()
+        return _IndexerPlan(self, x, qr, start_pos, offset, None).run()
 
-    #: smallest token count (b * s) for which the fused query projection is used
-    Q_PROJ_MIN_TOKENS = 64
+    def packed_weights(self):
+        """(wq_b, weights_proj) in dsa_indexer_projections' fragment order, packed once per
+        weight version (an in-place update moves a parameter's version counter; writes
+        through .data do not, so after those call refresh_packed_weights())."""
+        wq, wp = self.wq_b.weight, self.weights_proj.weight
+        tag = (wq.data_ptr(), wq._version, wp.data_ptr(), wp._version)
+        if self._packed is None or self._packed[0] != tag:
+            self._packed = (tag, _native.pack_projection_weights(wq, wp))
+        return self._packed[1]
+
+    def refresh_packed_weights(self) -> None:
+        """Drops the packed weights and the cached plan (after writes through .data)."""
+        self._packed = None
+        self._plan = None
 
     def _q_proj_fused(self, qr: torch.Tensor) -> bool:
-        """Whether q comes from dsa_indexer_q_proj instead of F.linear + RoPE in the score
-        kernel: q_lora_rank 256, rope_head_dim 32, bf16, at least 64 tokens. There the
-        kernel's natural-order k accumulation equals torch-ROCm's F.linear bit for bit
-        (tests/test_gpu_indexer_proj.py sweeps the token count); below 64 tokens hipBLASLt
-        switches to algorithms that reduce k in another order, so F.linear stays."""
-        w = self.wq_b.weight
-        return (qr.is_cuda and qr.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
-                and qr.shape[-1] == 256 and self.rope_head_dim == 32
-                and w.shape[0] % 256 == 0 and self.head_dim in (64, 128)
-                and qr.shape[0] * qr.shape[1] >= self.Q_PROJ_MIN_TOKENS)
+        """Whether q comes from a projection kernel (dsa_indexer_q_proj or
+        dsa_indexer_projections) rather than F.linear + RoPE in the score kernel."""
+        wq, wp = self.wq_b.weight, self.weights_proj.weight
+        return projection_route(
+            qr.shape[0] * qr.shape[1], qr.shape[-1], self.rope_head_dim, self.head_dim, wq.shape[0], self.dim,
+            wp.shape[0], qr.dtype == wq.dtype == torch.bfloat16, qr.is_cuda,
+            qr.is_cuda and _measured_build(qr.device)) != "torch"
+
+
+class _IndexerPlan:
+    """Everything Model.forward launches for one set of inputs, prepared once. Intermediate q
+    and wl buffers of the kernel paths are kept and reused by later calls of the plan: the
+    plan is keyed on the stream, and on one stream a call's projections start only after
+    the previous call's score kernel has read them."""
+
+    def __init__(self, model: Model, x: torch.Tensor, qr: torch.Tensor, start_pos: int, offset: int, key):
+        self.key = key
+        bsz, seqlen, _ = x.size()
+        ratio = model.compress_ratio
+        end_pos = start_pos + seqlen
+        n_cand = end_pos // ratio
+        k_out = min(model.index_topk, n_cand)
+        self.empty = (bsz, seqlen) if k_out <= 0 else None
+        self.device = x.device
+        if self.empty is not None:
+            return
+        self.x, self.qr = x, qr
+        self.wq, self.wp = model.wq_b.weight, model.weights_proj.weight
+        freqs = model.freqs_cis[start_pos:end_pos]
+        w_scale = model.softmax_scale * model.n_heads ** -0.5
+        hd, rd, mode = model.head_dim, model.rope_head_dim, model.rope_mode
+        self.route = model.route(x, qr)
+        kv = model.kv_cache
+        score_kw = dict(rope_head_dim=rd, n_cand=n_cand, k_out=k_out, ratio=ratio, causal=start_pos == 0,
+                        offset=offset, rope_mode=mode)
+        self.proj = None
+        if self.route == "both":
+            # q = RoPE(qr . wq_b^T) and wl = x . weights_proj^T in one launch
+            # (task2_v0_ref.py:129-132), bit-equal to F.linear + apply_rotary_emb here.
+            wq_p, wp_p = model.packed_weights()
+            self.proj, q_shape, wl_shape, self.proj_keep = _native.prepare_indexer_projections(
+                qr, wq_p, freqs, x, wp_p, hd, rd, mode)
+            self.q = torch.empty(q_shape, dtype=torch.bfloat16, device=x.device)
+            self.wl = torch.empty(wl_shape, dtype=torch.bfloat16, device=x.device)
+            self.proj.args[_native.PROJ_SLOT_Q] = self.q.data_ptr()
+            self.proj.args[_native.PROJ_SLOT_WL] = self.wl.data_ptr()
+            self.score = _native.prepare_indexer_score_topk(self.q, kv, self.wl, w_scale, None, **score_kw)
+        elif self.route == "q":
+            # q = RoPE(qr . wq_b^T) by dsa_indexer_q_proj; weights_proj stays F.linear.
+            prep = _native.prepare_indexer_q_proj(qr, self.wq, freqs, hd, rd, mode)
+            self.q = torch.empty(prep.out_shape, dtype=torch.bfloat16, device=x.device)
+            prep.launch.args[prep.out_slot] = self.q.data_ptr()
+            self.proj, self.proj_keep = prep.launch, prep.keep
+            wl0 = torch.empty(bsz, seqlen, model.n_heads, dtype=torch.bfloat16, device=x.device)
+            self.score = _native.prepare_indexer_score_topk(self.q, kv, wl0, w_scale, None, **score_kw)
+        else:
+            # F.linear for both (task2_v0_ref.py:129-132); the score kernel applies RoPE.
+            self.heads = (model.n_local_heads, hd)
+            q0 = torch.empty(bsz, seqlen, model.n_local_heads, hd, dtype=torch.bfloat16, device=x.device)
+            wl0 = torch.empty(bsz, seqlen, model.n_heads, dtype=torch.bfloat16, device=x.device)
+            self.score = _native.prepare_indexer_score_topk(q0, kv, wl0, w_scale, freqs, **score_kw)
+
+    def run(self) -> torch.Tensor:
+        if self.empty is not None:
+            return torch.empty(*self.empty, 0, dtype=torch.int64, device=self.device)
+        args = self.score.launch.args
+        if self.route == "both":
+            self.proj()
+        elif self.route == "q":
+            self.proj()
+            wl = F.linear(self.x, self.wp)
+            args[_native.SCORE_SLOT_WL] = wl.data_ptr()
+        else:
+            q = F.linear(self.qr, self.wq).unflatten(-1, self.heads)
+            wl = F.linear(self.x, self.wp)
+            args[_native.SCORE_SLOT_Q] = q.data_ptr()
+            args[_native.SCORE_SLOT_WL] = wl.data_ptr()
+        # (The fresh q / wl tensors of the torch paths are released when this returns; the
+        # caching allocator hands their memory only to later work on this stream.)
+        return self.score.run()
 
 
 ModelNew = Model

@@ -12,9 +12,9 @@ minus the flushes alone, so that cold and hot calls are timed the same way; the
 headline also gives one call timed alone after a flush):
   task1_c1      configs[0] on the GPU, beside the reference path on the host CPU;
   task1_c4      the true-gather kernel at configs[3] (MFMA-bound);
-  task2         configs[2]: Model.forward (query projection + RoPE kernel, the
-                weights projection in torch, the fused score / top-k kernel), the
-                fused kernel and the projection kernel alone with their rooflines,
+  task2         configs[2]: Model.forward (one launch for both projections, q with
+                RoPE and the head weights, then the fused score / top-k kernel), the
+                fused kernel and the projections kernel alone with their rooflines,
                 and the reference path on the host CPU;
   dsa_layer_c5  configs[4]: the wide indexer, sparse MLA, and the whole prefill layer
                 (indexer Model.forward whose int64 top-2048 feeds sparse MLA);
@@ -379,7 +379,7 @@ def main():
             for p5 in (ix5.wq_b.weight, ix5.weights_proj.weight):
                 p5.copy_((torch.randn(p5.shape, generator=g5) * 0.02).to(torch.bfloat16))
         x5, qr5, sp5, off5 = t2.get_c5_inputs(device=dev)
-        n5 = max(3, a.steps // 10)
+        n5 = max(10, a.steps // 5)
         with torch.no_grad():
             _warm(torch, lambda: ix5(x5, qr5, sp5, off5), 2, 0.2)
             ms_ix = _events_time(torch, lambda: ix5(x5, qr5, sp5, off5), n5, stream)
@@ -454,13 +454,13 @@ def main():
             _warm(torch, lambda: m2(x, qr, sp, off), a.warmup, 0.2)
             ms2 = _events_time(torch, lambda: m2(x, qr, sp, off), a.steps, stream)
             m2_cold = cold(lambda: m2(x, qr, sp, off), 20)
-            # The kernels as Model.forward runs them: q projected and rotated by
-            # dsa_indexer_q_proj, wl by F.linear, then the fused score / top-k kernel.
+            # The kernels as Model.forward runs them: both projections in one launch
+            # (q rotated, and the head weights), then the fused score / top-k kernel.
             fr = m2.freqs_cis[:2600]
-            assert m2._q_proj_fused(qr)
-            pfn = lambda: _native.indexer_q_proj(qr, m2.wq_b.weight, fr, 64, 32)
-            qp = pfn()
-            wl = torch.nn.functional.linear(x, m2.weights_proj.weight)
+            assert m2.route(x, qr) == "both"
+            pq, pw = m2.packed_weights()
+            pfn = lambda: _native.indexer_projections(qr, pq, fr, x, pw, 64, 32)
+            qp, wl = pfn()
             scale = 64 ** -0.5 * 16 ** -0.5
             kfn = lambda: _native.indexer_score_topk(qp, m2.kv_cache, wl, scale, None, 32, 650, 128, 4, True, 0)
             _warm(torch, kfn, 3, 0.1)
@@ -468,14 +468,20 @@ def main():
             k_cold = cold(kfn, 20)
             _warm(torch, pfn, 3, 0.1)
             msp = _events_time(torch, pfn, a.steps, stream)
-            # torch's projection for comparison (F.linear; RoPE then runs inside the score kernel)
-            lfn = lambda: torch.nn.functional.linear(qr, m2.wq_b.weight)
+            # torch's two projections for comparison (F.linear; RoPE would then run inside the
+            # score kernel), and the query-projection kernel alone (the 'q' route)
+            lfn = lambda: (torch.nn.functional.linear(qr, m2.wq_b.weight),
+                           torch.nn.functional.linear(x, m2.weights_proj.weight))
             _warm(torch, lfn, 3, 0.1)
             msl = _events_time(torch, lfn, a.steps, stream)
+            qfn = lambda: _native.indexer_q_proj(qr, m2.wq_b.weight, fr, 64, 32)
+            _warm(torch, qfn, 3, 0.1)
+            msq = _events_time(torch, qfn, a.steps, stream)
         kb = t2_kernel_bytes()
-        proj_flop = 2 * 8 * 2600 * 1024 * 256
-        # qr read, wq_b read, q written, the RoPE table rows read
-        proj_bytes = 8 * 2600 * 256 * 2 + 1024 * 256 * 2 + 8 * 2600 * 1024 * 2 + 2600 * 16 * 8
+        proj_flop = 2 * 8 * 2600 * (1024 * 256 + 16 * 1024)
+        # qr and x read, both weights read, q and wl written, the RoPE table rows read
+        proj_bytes = (8 * 2600 * 256 * 2 + 8 * 2600 * 1024 * 2 + 1024 * 256 * 2 + 16 * 1024 * 2
+                      + 8 * 2600 * 1024 * 2 + 8 * 2600 * 16 * 2 + 2600 * 16 * 8)
         score_flop = 2 * 16 * 64 * sum(((t + 1) // 4) for t in range(2600)) * 8
         result["task2"] = {
             "workload": "task2_indexer configs[2]: x[8,2600,1024], qr[8,2600,256], kv_cache[8,650,64], "
@@ -493,15 +499,18 @@ def main():
             # fractions are reported, the HBM one as "roofline".
             "roofline": _roofline_hbm(kb, msk, _traffic("ix_score_topk_kernel")),
             "roofline_mfma": _roofline_mfma(score_flop, msk),
-            "q_proj": {
-                "kernel": "ix_proj_k256_kernel (q = RoPE(qr . wq_b^T), bit-equal to F.linear + apply_rotary_emb)",
+            "projections": {
+                "kernel": "ix_proj2_kernel (one launch: q = RoPE(qr . wq_b^T) and wl = x . weights_proj^T, "
+                          "bit-equal to F.linear + apply_rotary_emb and F.linear)",
                 "us": round(msp * 1e3, 2),
                 "flop": proj_flop,
                 "TFLOPs": round(proj_flop / (msp * 1e-3) / 1e12, 1),
                 "bytes": proj_bytes,
                 "GBps": round(proj_bytes / (msp * 1e-3) / 1e9, 1),
+                "roofline": _roofline_hbm(proj_bytes, msp, _traffic("ix_proj2_kernel")),
                 "roofline_mfma": _roofline_mfma(proj_flop, msp),
-                "torch_f_linear_us": round(msl * 1e3, 2),
+                "torch_two_f_linear_us": round(msl * 1e3, 2),
+                "q_proj_kernel_alone_us": round(msq * 1e3, 2),
             },
         }
         t2_cpu_inputs = (m2.wq_b.weight.detach().cpu(), m2.weights_proj.weight.detach().cpu(),

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 2
+#define DSA_ABI_VERSION 3
 
 #define DSA_OK 0
 #define DSA_ERR_NULL (-1)        /* a required pointer is NULL */
@@ -240,7 +240,7 @@ int dsa_indexer_score_topk_ws(const void* q, const void* kv_cache, int64_t kv_ba
  * call is made, so it can be used where the caller cannot allocate (inside HIP graph
  * capture, allocation-free serving loops).
  * No counterpart in the reference: an addition for callers that cannot allocate;
- * it computes what dsa_indexer_score_topk does (reference/task2_v0_ref.py:131-143).
+ * it computes what dsa_indexer_score_topk does.
  */
 #define DSA_INDEXER_NOALLOC_MAX_BYTES (INT64_C(16) << 20)
 int dsa_indexer_score_topk_noalloc(const void* q, const void* kv_cache, int64_t kv_batch_stride,
@@ -287,6 +287,52 @@ int dsa_indexer_scores(const void* q, const void* kv_cache, int64_t kv_batch_str
 int dsa_indexer_q_proj(const void* qr, const void* wq, const void* freqs_cis, int32_t rope_mode,
                        void* q, int64_t m, int64_t n, int64_t k, int64_t head_dim, int64_t rd,
                        int64_t s_len, void* stream);
+
+/*
+ * Fragment packing of the indexer's projection weights for dsa_indexer_projections: a
+ * permutation of the same bytes into the order the kernel's registers take them, done
+ * once per weight version (the Ascend submission prepares its matmul executors once the
+ * same way, src/task2_indexer.py:764-804 prepare_c2).
+ *   wq           bf16 [n, k]      wq_b.weight (reference/task2_v0_ref.py:116), k == 256, n % 64 == 0
+ *   wproj        bf16 [n_w, dim]  weights_proj.weight (:117), n_w % 16 == 0, dim % 32 == 0
+ *   wq_packed    n * k bf16 words; wproj_packed n_w * dim bf16 words
+ * Either pair (wq, wq_packed) or (wproj, wproj_packed) may be NULL, NULL. Pointers 16-byte
+ * aligned. Layouts: wq_packed fragment f = ((r * 2 + i) * 16 + ks) * 64 + lane (16 bytes)
+ * holds wq[64 r + 32 i + lane % 32][16 ks + 8 (lane / 32) .. + 7]; wproj_packed fragment
+ * e = (hg * (dim / 32) + ks) * 64 + lane holds wproj[16 hg + lane % 16][32 ks + 8 (lane / 16) .. + 7].
+ */
+int dsa_indexer_pack_projection_weights(const void* wq, int64_t n, int64_t k, const void* wproj,
+                                        int64_t n_w, int64_t dim, void* wq_packed,
+                                        void* wproj_packed, void* stream);
+
+/*
+ * Both projections of the indexer in one launch (reference/task2_v0_ref.py:129-132):
+ *   q  = apply_rotary_emb(qr . wq^T)  on the last rd channels of every head   (:129-131)
+ *   wl = x . wproj^T                                                       (:132, before the scale)
+ * Replaces the two F.linear calls and the RoPE; the Ascend submission runs weights_proj on a
+ * second stream beside the query path (src/task2_indexer.py:805-839 go_c2_ovl, :871-879
+ * go_t2); here both run in one grid, with no stream or event calls. Both products
+ * accumulate in fp32 over k in ascending order and round once to bf16; RoPE as in
+ * dsa_indexer_q_proj. That equals torch-ROCm's F.linear where hipBLASLt runs a kernel
+ * without split-k: for wq (k = 256) from 17 tokens up, for weights_proj (k = 1024, 16
+ * outputs) only from about 20,000 tokens (below, hipBLASLt sums k over 4 wave groups);
+ * the drop-in Model calls this entry point only inside the token range its GPU sweep covers.
+ *
+ *   qr            bf16 [m, k]      m = b * s_len token rows, k == 256
+ *   wq_packed     from dsa_indexer_pack_projection_weights, n = heads * head_dim, n % 256 == 0
+ *   freqs_cis     complex64 [s_len, rd/2] rows of positions start_pos .. (16-byte aligned), or NULL
+ *   rope_mode     DSA_ROPE_TORCH_ROCM or DSA_ROPE_CPU
+ *   q             bf16 [m, n] output (RoPE applied)
+ *   x             bf16 [m, dim], dim == 1024
+ *   wproj_packed  from dsa_indexer_pack_projection_weights, n_w == 16
+ *   wl            bf16 [m, n_w] output (8-byte aligned)
+ * Requirements: head_dim == 64, rd == 32 when freqs_cis != NULL, m % s_len == 0,
+ * m * n * 2 and m * dim * 2 below 2^32; pointers 16-byte aligned unless stated.
+ */
+int dsa_indexer_projections(const void* qr, const void* wq_packed, const void* freqs_cis,
+                            int32_t rope_mode, void* q, const void* x, const void* wproj_packed,
+                            void* wl, int64_t m, int64_t n, int64_t k, int64_t dim, int64_t n_w,
+                            int64_t head_dim, int64_t rd, int64_t s_len, void* stream);
 
 #ifdef __cplusplus
 }

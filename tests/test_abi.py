@@ -256,3 +256,41 @@ def test_q_proj_host_checks():
     assert f(m=0) == 0
     assert f(q=None) == -1
     assert f(fr=24) == -6          # table not 16-byte aligned
+
+
+def _proj(lib, **kw):
+    a = dict(qr=16, wq=16, fr=16, mode=1, q=16, x=16, wp=16, wl=16, m=64, n=1024, k=256, dim=1024, n_w=16,
+             d=64, rd=32, s=64)
+    a.update(kw)
+    return lib.dsa_indexer_projections(a["qr"], a["wq"], a["fr"], a["mode"], a["q"], a["x"], a["wp"], a["wl"],
+                                       a["m"], a["n"], a["k"], a["dim"], a["n_w"], a["d"], a["rd"], a["s"], None)
+
+
+def test_projections_host_checks():
+    lib = _native.load()
+    assert _proj(lib, m=-1) == -2
+    assert _proj(lib, n=1000) == -2                 # n % head_dim
+    assert _proj(lib, m=65) == -2                   # m % s_len
+    assert _proj(lib, k=512) == -3                  # k = 256 only
+    assert _proj(lib, d=128, n=1024) == -3          # head_dim 64 only
+    assert _proj(lib, dim=2048) == -3 and _proj(lib, n_w=32) == -3
+    assert _proj(lib, rd=64) == -3 and _proj(lib, mode=5) == -3
+    assert _proj(lib, rd=33) == -2
+    assert _proj(lib, m=0) == 0
+    for name in ("qr", "wq", "q", "x", "wp", "wl"):
+        assert _proj(lib, **{name: None}) == -1, name
+    assert _proj(lib, x=8) == -6 and _proj(lib, wl=4) == -6 and _proj(lib, fr=8) == -6
+    assert _proj(lib, m=2 ** 21, s=2 ** 21) == -3   # 32-bit buffer offsets
+
+
+def test_pack_projection_weights_host_checks():
+    lib = _native.load()
+    f = lib.dsa_indexer_pack_projection_weights
+    assert f(None, 0, 0, None, 0, 0, None, None, None) == 0          # nothing to pack
+    assert f(16, 1024, 256, None, 0, 0, None, None, None) == -1      # wq without its output
+    assert f(16, 1024, 512, None, 0, 0, 16, None, None) == -3        # k = 256 only
+    assert f(16, 1000, 256, None, 0, 0, 16, None, None) == -3        # n % 64
+    assert f(16, -1, 256, None, 0, 0, 16, None, None) == -2
+    assert f(None, 0, 0, 16, 20, 1024, None, 16, None) == -3         # n_w % 16
+    assert f(None, 0, 0, 16, 16, 1000, None, 16, None) == -3         # dim % 32
+    assert f(8, 1024, 256, None, 0, 0, 16, None, None) == -6

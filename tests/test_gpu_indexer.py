@@ -174,6 +174,14 @@ SMALL = [
     (1, 63, 1500, 2, 128, 650),
     (1, 64, 1500, 2, 128, 650),
     (5, 13, 100, 0, 32, 650),
+    # either side of the one-launch projections' lower end (16,385 tokens), inside the
+    # range with other batch splits, a mid-sequence chunk, and near its upper end (65,498)
+    # (the 16-head score kernel takes up to 2048 candidates: end_pos // 4 <= 2048)
+    (2, 8192, 0, 0, 128, 2048),
+    (5, 3277, 0, 1, 128, 820),
+    (5, 3333, 0, 0, 64, 834),
+    (4, 5000, 2000, 4, 128, 1750),
+    (8, 8187, 0, 0, 32, 2047),
 ]
 
 
@@ -296,3 +304,30 @@ def test_score_stage_matches_torch(gpu, seqlen, start_pos):
         _say("first bad row", r0, "n_r", int(n_r[r0]), "got", idx.reshape(-1, k)[r0][:16].tolist(),
              "want", want_idx[r0][:16].tolist())
     assert not bad.any(), int(bad.sum())
+
+
+def test_model_launch_plan_reuse(gpu):
+    """Model.forward's cached plan (one launch of both projections at configs[2]): repeated
+    calls agree and return fresh tensors; new inputs, new input contents under the same
+    pointers, and in-place weight updates (new packed weights) each match the oracle."""
+    args = t2._make_args()
+    m, r = _pair(args, 31, 8, 650, gpu)
+    torch.manual_seed(32)
+    x, qr, sp, off = t2.get_inputs(device=gpu)
+    assert m.route(x, qr) == "both"
+    a, b = m(x, qr, sp, off), m(x, qr, sp, off)
+    assert a.data_ptr() != b.data_ptr()
+    _check_equal(a, b, "plan repeat")
+    _check_equal(b, r(x, qr, sp, off), "plan vs oracle")
+    x2, qr2, _, _ = t2.get_inputs(device=gpu)
+    _check_equal(m(x2, qr2, sp, off), r(x2, qr2, sp, off), "plan new inputs")
+    x2.copy_(x)
+    _check_equal(m(x2, qr2, sp, off), r(x2, qr2, sp, off), "plan new contents")
+    g = torch.Generator().manual_seed(33)
+    with torch.no_grad():
+        for p in (m.wq_b.weight, m.weights_proj.weight):
+            p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(torch.bfloat16))
+    r.wq_b.weight.data.copy_(m.wq_b.weight.data)
+    r.weights_proj.weight.data.copy_(m.weights_proj.weight.data)
+    _check_equal(m(x2, qr2, sp, off), r(x2, qr2, sp, off), "plan new weights")
+    _check_equal(m(x2, qr2, 0, 3), r(x2, qr2, 0, 3), "plan new offset")

@@ -5,7 +5,8 @@ the same GPU. The reference path here is the oracle's op-for-op restatement of t
 reference modules (oracle/sparse_attn.py, oracle/indexer.py) run by torch-ROCm.
 Times are hipEvent medians over a few calls; the test prints them and requires the
 HIP path to be faster at the benchmark configurations (configs[1], [2], [3], [4]).
-The budget tests hold the kernels to fixed times at the full configurations.
+The budget tests hold the kernels at the full configurations to times relative to a
+calibration (a device copy, a bf16 matmul) measured in the same process.
 """
 import statistics
 
@@ -56,25 +57,56 @@ def _settled_us(fn, reps, min_seconds=0.3):
     return a.elapsed_time(z) * 1e3 / reps
 
 
-# Kernel-time budgets in microseconds (hot caches, settled clock): a regression of the
-# kernels past these fails. Measured values are printed. Each sits ~7-15 % above the
-# slowest box of the pool seen so far (C2 117-120, C3 kernel with in-kernel RoPE 48-51,
-# projection 18-20, Model.forward 73-76, C4 383-423, C5 sparse MLA 5,070-5,700 us), so
-# that box-to-box spread alone does not fail the suite.
-BUDGET_US = {"c2": 128.0, "c3_kernel": 58.0, "c3_q_proj": 23.0, "c3_model": 84.0, "c4": 470.0,
-             "c5_mla": 6300.0}
+# Budgets relative to a calibration timed in the same process, so that the clock and
+# memory speed of the box cancel: the HBM-bound Task1 kernel against torch's device copy of
+# the configs[1] q (340.8 MB read and written), every other kernel (matrix cores, VALU, the
+# clock) against a bf16 [8192 x 8192] x [8192 x 8192] torch.matmul. A regression past
+# ratio x calibration fails; each ratio sits 5 % above the largest of three measured on this
+# build (configs[1]: 0.99, a 125 us equivalent at the copy's 126 us). Measured (copy 125.6 -
+# 126.8 us, matmul 794 - 801 us): c2 0.935 - 0.944, c3 kernel 0.0548 - 0.0553, c3 projections
+# 0.0282 - 0.0287, c3 Model.forward 0.0826 - 0.0838, c4 0.502 - 0.511, c5 MLA 6.50 - 6.61.
+RATIO_BUDGET = {"c2": ("copy", 0.99), "c3_kernel": ("matmul", 0.0581), "c3_proj": ("matmul", 0.0301),
+                "c3_model": ("matmul", 0.0880), "c4": ("matmul", 0.536), "c5_mla": ("matmul", 6.94)}
 
 
-def test_budget_task1_c2(gpu):
+@pytest.fixture(scope="module")
+def calib(gpu):
+    return calibrate(gpu)
+
+
+def calibrate(gpu):
+    """The calibration times (us) of this process: {'copy': ..., 'matmul': ...}."""
+    torch.manual_seed(0)
+    src = torch.randn(8, 2600, 64, 128, device=gpu).to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    copy_us = _settled_us(lambda: dst.copy_(src), 50)
+    del src, dst
+    a = torch.randn(8192, 8192, device=gpu).to(torch.bfloat16)
+    b = torch.randn(8192, 8192, device=gpu).to(torch.bfloat16)
+    mm_us = _settled_us(lambda: torch.matmul(a, b), 20)
+    del a, b
+    torch.cuda.empty_cache()
+    print(f"[calibration] copy {copy_us:.1f} us, matmul {mm_us:.1f} us", flush=True)
+    return {"copy": copy_us, "matmul": mm_us}
+
+
+def _check_budget(name, us, calib):
+    base, ratio = RATIO_BUDGET[name]
+    got = us / calib[base]
+    print(f"[budget {name}] {us:.1f} us = {got:.4f} x {base} ({calib[base]:.1f} us); budget {ratio:.4f} "
+          f"({ratio * calib[base]:.1f} us)", flush=True)
+    assert got <= ratio, f"{name}: {us:.1f} us is {got:.4f} x {base}, budget {ratio:.4f}"
+
+
+def test_budget_task1_c2(gpu, calib):
     torch.manual_seed(42)
     q, kv, idx = [x.to(gpu) for x in t1.get_inputs()]
     m = t1.Model(*t1.get_init_inputs()).to(gpu)
     us = _settled_us(lambda: m(q, kv, idx), 50)
-    print(f"[budget c2] {us:.1f} us (budget {BUDGET_US['c2']})", flush=True)
-    assert us <= BUDGET_US["c2"]
+    _check_budget("c2", us, calib)
 
 
-def test_budget_task2_c3_kernel(gpu):
+def test_budget_task2_c3_kernel(gpu, calib):
     from ascendc_kernel_amd import _native
     torch.manual_seed(42)
     m = t2.Model(*t2.get_init_inputs(device=gpu)).to(gpu)
@@ -83,42 +115,39 @@ def test_budget_task2_c3_kernel(gpu):
         q = torch.nn.functional.linear(qr, m.wq_b.weight).unflatten(-1, (16, 64)).contiguous()
         wl = torch.nn.functional.linear(x, m.weights_proj.weight)
         fn = lambda: _native.indexer_score_topk(q, m.kv_cache, wl, 64 ** -0.5 * 16 ** -0.5,
-                                                m.freqs_cis[:2600], 32, 650, 128, 4, True, 0)
+                                                None, 32, 650, 128, 4, True, 0)
         us = _settled_us(fn, 50)
-    print(f"[budget c3 fused kernel] {us:.1f} us (budget {BUDGET_US['c3_kernel']})", flush=True)
-    assert us <= BUDGET_US["c3_kernel"]
+    _check_budget("c3_kernel", us, calib)
 
 
-def test_budget_task2_c3_q_proj_and_model(gpu):
-    """The query projection + RoPE kernel and the whole Model.forward at configs[2]."""
+def test_budget_task2_c3_projections_and_model(gpu, calib):
+    """The one-launch projections (q with RoPE, and the head weights) and the whole
+    Model.forward at configs[2]."""
     from ascendc_kernel_amd import _native
     torch.manual_seed(42)
     m = t2.Model(*t2.get_init_inputs(device=gpu)).to(gpu)
     x, qr, sp, off = t2.get_inputs(device=gpu)
-    assert m._q_proj_fused(qr)
+    assert m.route(x, qr) == "both"
+    pq, pw = m.packed_weights()
     with torch.no_grad():
-        us_p = _settled_us(lambda: _native.indexer_q_proj(qr, m.wq_b.weight, m.freqs_cis[:2600], 64, 32), 50)
+        us_p = _settled_us(lambda: _native.indexer_projections(qr, pq, m.freqs_cis[:2600], x, pw, 64, 32), 50)
         us_m = _settled_us(lambda: m(x, qr, sp, off), 50)
-    print(f"[budget c3 q_proj] {us_p:.1f} us (budget {BUDGET_US['c3_q_proj']}); "
-          f"[budget c3 Model.forward] {us_m:.1f} us (budget {BUDGET_US['c3_model']})", flush=True)
-    assert us_p <= BUDGET_US["c3_q_proj"]
-    assert us_m <= BUDGET_US["c3_model"]
+    _check_budget("c3_proj", us_p, calib)
+    _check_budget("c3_model", us_m, calib)
 
 
-def test_budget_task1_c4(gpu):
+def test_budget_task1_c4(gpu, calib):
     q, kv, idx = t1.get_gather_inputs(device=gpu)
     m = t1.Model(64, 128).to(gpu)
     us = _settled_us(lambda: m(q, kv, idx), 10)
-    print(f"[budget c4] {us:.1f} us (budget {BUDGET_US['c4']})", flush=True)
-    assert us <= BUDGET_US["c4"]
+    _check_budget("c4", us, calib)
 
 
-def test_budget_c5_mla(gpu):
+def test_budget_c5_mla(gpu, calib):
     q, kv, idx = t1.get_mla_inputs(device=gpu)
     m = t1.Model(128, 576, v_dim=512).to(gpu)
-    us = _settled_us(lambda: m(q, kv, idx), 3, 0.2)
-    print(f"[budget c5 sparse MLA] {us:.1f} us (budget {BUDGET_US['c5_mla']})", flush=True)
-    assert us <= BUDGET_US["c5_mla"]
+    us = _settled_us(lambda: m(q, kv, idx), 5, 0.2)
+    _check_budget("c5_mla", us, calib)
 
 
 def test_task1_c2_faster_than_torch_path(gpu):

@@ -173,12 +173,33 @@ def test_fixture_masked_needs_gather_variant(gpu):
     idx = torch.from_numpy(f["idx"]).to(gpu)
     sink = torch.from_numpy(f["sink"]).to(gpu)
     _say("case fixture masked (gather)")
-    try:
-        out = _native.sparse_attn_fwd(q, kv, idx, sink, float(f["scale"]))
-    except _native.DsaError as e:
-        assert e.code == -3
-        pytest.skip("gather variant not built yet")
+    out = _native.sparse_attn_fwd(q, kv, idx, sink, float(f["scale"]))
     _compare(out.cpu(), bf16_from_bits(f["out"]), "masked-fixture")
+
+
+def test_module_launch_plan_reuse(gpu):
+    """Model.forward's cached launch: repeated calls give identical fresh outputs; new input
+    tensors (other pointers), an in-place update of attn_sink and int64 indices each give the
+    oracle's result of their own inputs, not the cached ones."""
+    from ascendc_kernel_amd import task1_sparse_attn as t1
+    g = torch.Generator().manual_seed(61)
+    m = t1.Model(64, 128).to(gpu)
+    mk = lambda: (torch.randn(2, 40, 64, 128, generator=g).to(torch.bfloat16).to(gpu),
+                  torch.randn(2, 32, 128, generator=g).to(torch.bfloat16).to(gpu),
+                  torch.randint(-2, 32, (2, 40, 16), generator=g, dtype=torch.int32).to(gpu))
+    q, kv, idx = mk()
+    a, b = m(q, kv, idx), m(q, kv, idx)
+    assert a.data_ptr() != b.data_ptr() and torch.equal(a.view(torch.int16), b.view(torch.int16))
+    _compare(b, osa.sparse_attn_ref(q, kv, m.attn_sink, idx, m.softmax_scale), "plan repeat")
+    q2, kv2, idx2 = mk()
+    _compare(m(q2, kv2, idx2), osa.sparse_attn_ref(q2, kv2, m.attn_sink, idx2, m.softmax_scale), "plan new inputs")
+    q2.copy_(q)  # same pointers as the cached plan, new contents: read at launch
+    _compare(m(q2, kv2, idx2), osa.sparse_attn_ref(q2, kv2, m.attn_sink, idx2, m.softmax_scale), "plan new contents")
+    with torch.no_grad():
+        m.attn_sink.copy_(torch.linspace(-2, 2, 64))
+    _compare(m(q2, kv2, idx2), osa.sparse_attn_ref(q2, kv2, m.attn_sink, idx2, m.softmax_scale), "plan new sink")
+    i64 = idx2.long()
+    _compare(m(q2, kv2, i64), osa.sparse_attn_ref(q2, kv2, m.attn_sink, idx2, m.softmax_scale), "plan int64")
 
 
 GATHER_CASES = [

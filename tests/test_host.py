@@ -95,3 +95,142 @@ def test_task1_gather_inputs_properties():
                 assert bool((valid >= 0).all()) and bool((valid <= t).all())
                 assert len(set(valid.tolist())) == n
                 assert bool((row[n:] == -1).all())
+
+
+# ---------------------------------------------------------------- projection routing
+def test_projection_route_boundaries():
+    """Model.forward uses a kernel for the projections only at token counts where its rounding
+    was measured equal to F.linear (the interval tables), and only on the measured build."""
+    c3 = dict(q_lora_rank=256, rope_head_dim=32, head_dim=64, n_q=1024, dim=1024, n_w=16, bf16=True,
+              on_gpu=True, build_ok=True)
+    r = lambda m, **kw: t2.projection_route(m, **{**c3, **kw})
+    assert r(8 * 2600) == "both"                       # configs[2]
+    for a, b in t2.WL_EQUAL:
+        for m in (a, b):
+            if m >= t2.Q_PROJ_MIN_TOKENS:
+                assert r(m) == ("both" if t2._within(m, t2.Q_EQUAL) else "torch")
+    for a, b in t2.Q_EQUAL:
+        for m in (a - 1, a, b, b + 1):
+            inq = t2._within(m, t2.Q_EQUAL) and m >= t2.Q_PROJ_MIN_TOKENS
+            want = ("both" if t2._within(m, t2.WL_EQUAL) else "q") if inq else "torch"
+            assert r(m) == want, m
+    assert r(32768) == "both" and r(32769) == "torch"   # hipBLASLt splits wq_b's k sum above 32,768
+    assert r(16384) == "q" and r(16385) == "both"
+    assert r(63) == "torch" and r(64) == r(140) == "both" and r(141) == "q"   # weights_proj: 17 .. 140
+    assert r(8 * 2600, build_ok=False) == "torch"      # another torch / hipBLASLt build or CU count
+    assert r(8 * 2600, on_gpu=False) == r(8 * 2600, bf16=False) == "torch"
+    assert r(8 * 2600, dim=2048) == r(8 * 2600, n_w=32) == "q"
+    assert r(8 * 2600, head_dim=128) == "q"            # the one-launch kernel is head_dim 64 only
+    assert r(8 * 2600, q_lora_rank=1536) == r(8 * 2600, rope_head_dim=64) == "torch"   # configs[4]
+    assert r(1) == "torch"                             # decode
+
+
+def test_projection_tables_match_measurement():
+    """Q_EQUAL / WL_EQUAL are the intervals tests/golden/projection_ranges.json holds (written by
+    tests/golden/measure_projection_ranges.py on the build MEASURED_TORCH names), sorted and
+    disjoint."""
+    import json
+    import os
+    from conftest import GOLDEN
+    with open(os.path.join(GOLDEN, "projection_ranges.json")) as f:
+        r = json.load(f)
+    assert (r["torch"], r["hip"]) == t2.MEASURED_TORCH and r["cus"] == t2.MEASURED_CUS
+    assert [tuple(v) for v in r["q_equal"]] == list(t2.Q_EQUAL)
+    assert [tuple(v) for v in r["wl_equal"]] == list(t2.WL_EQUAL)
+    for table in (t2.Q_EQUAL, t2.WL_EQUAL):
+        assert all(a <= b for a, b in table)
+        assert all(table[i][1] + 1 < table[i + 1][0] for i in range(len(table) - 1))
+        for a, b in table:
+            assert t2._within(a, table) and t2._within(b, table)
+            assert not t2._within(a - 1, table) and not t2._within(b + 1, table)
+
+
+# ---------------------------------------------------------------- steady-state launch plans
+class _FakePrepared:
+    """Stands in for _native.Prepared, which holds its inputs (`keep`) so that their memory
+    cannot go to another tensor at the same address while the plan's key names it."""
+
+    def __init__(self, log, shape, keep):
+        self.log, self.shape, self.keep = log, shape, keep
+
+    def run(self):
+        self.log.append("run")
+        return torch.zeros(self.shape)
+
+
+def _fake_native(monkeypatch, log):
+    from ascendc_kernel_amd import _native
+    monkeypatch.setattr(_native, "stream_handle", lambda dev: 1234)
+    monkeypatch.setattr(_native, "prepare_sparse_attn",
+                        lambda q, kv, idx, sink, scale, variant:
+                        log.append("prepare") or _FakePrepared(log, q.shape, (q, kv, idx)))
+    monkeypatch.setattr(_native, "prepare_sparse_mla",
+                        lambda q, kv, idx, sink, scale, v:
+                        log.append("prepare") or _FakePrepared(log, q.shape, (q, kv, idx)))
+
+
+def test_task1_plan_cache(monkeypatch):
+    """The same inputs reuse the prepared launch; a changed pointer, shape, index dtype or an
+    in-place update of attn_sink prepares anew (the cache is exercised on CPU tensors with the
+    C ABI stubbed out)."""
+    from ascendc_kernel_amd import _native
+    log = []
+    _fake_native(monkeypatch, log)
+    m = t1.Model(64, 128)
+    monkeypatch.setattr(_native, "PLAN_DEVICE_TYPE", "cpu")
+    q = torch.zeros(1, 40, 64, 128, dtype=torch.bfloat16)
+    kv = torch.zeros(1, 32, 128, dtype=torch.bfloat16)
+    idx = torch.zeros(1, 40, 16, dtype=torch.int32)
+    for _ in range(3):
+        m(q, kv, idx)
+    assert log.count("prepare") == 1 and log.count("run") == 3
+    m(q.clone(), kv, idx)                              # another q pointer
+    assert log.count("prepare") == 2
+    m(q, kv, idx)                                      # back to the first: the cache holds one plan
+    assert log.count("prepare") == 3
+    m(q[:, :20].contiguous(), kv, idx[:, :20].contiguous())   # other shapes
+    assert log.count("prepare") == 4
+    m(q, kv, idx)
+    with torch.no_grad():
+        m.attn_sink.add_(1.0)                          # in-place parameter update
+    m(q, kv, idx)
+    assert log.count("prepare") == 6
+    m(q, kv, idx.long())                               # int64 indices
+    assert log.count("prepare") == 7
+    m(q, kv, idx.long().contiguous())
+    assert log.count("prepare") == 8                   # a new int64 tensor, new pointer
+
+
+def test_task2_plan_cache(monkeypatch):
+    """Model.forward of Task2 keeps one plan per (inputs, positions, weights, cache, stream):
+    changing start_pos, offset, an input pointer or a weight's version builds a new one."""
+    built = []
+
+    class FakePlan:
+        def __init__(self, model, x, qr, start_pos, offset, key):
+            self.key = key
+            built.append((start_pos, offset))
+
+        def run(self):
+            return torch.zeros(1)
+
+    from ascendc_kernel_amd import _native
+    monkeypatch.setattr(t2, "_IndexerPlan", FakePlan)
+    monkeypatch.setattr(_native, "stream_handle", lambda dev: 99)
+    monkeypatch.setattr(_native, "PLAN_DEVICE_TYPE", "cpu")
+    a = t2._make_args()
+    m = t2.Model(a, torch.ones(2600, 16, dtype=torch.complex64), torch.zeros(8, 650, 64, dtype=torch.bfloat16))
+    x = torch.zeros(1, 64, 1024, dtype=torch.bfloat16)
+    qr = torch.zeros(1, 64, 256, dtype=torch.bfloat16)
+    for _ in range(3):
+        m(x, qr, 0, 0)
+    assert built == [(0, 0)]
+    m(x, qr, 64, 0)
+    m(x, qr, 64, 5)
+    assert built == [(0, 0), (64, 0), (64, 5)]
+    m(x.clone(), qr, 64, 5)
+    assert len(built) == 4
+    with torch.no_grad():
+        m.weights_proj.weight.mul_(2)
+    m(x.clone(), qr, 64, 5)
+    assert len(built) == 5
