@@ -62,3 +62,18 @@ def test_noalloc_matches_workspace_entry_point(gpu):
                                           use_workspace=True)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"call {i}: {int((got != want).any(-1).sum())} rows differ"
+
+
+def test_noalloc_first_call_inside_graph_capture(gpu):
+    """The header's claim that the entry point works under HIP graph capture, with its first
+    call of the process inside the capture: run in a fresh child process
+    (tests/noalloc_capture_child.py), which replays the graph over new inputs and checks every
+    replay against the workspace entry point and that the replays allocate nothing."""
+    import os
+    import subprocess
+    import sys
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture_child.py")
+    _say("noalloc first call inside graph capture (child process)")
+    r = subprocess.run([sys.executable, "-u", child], capture_output=True, text=True, timeout=240)
+    _say(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK")
