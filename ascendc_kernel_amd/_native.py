@@ -14,7 +14,7 @@ import torch
 
 from . import build as _build
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DSA_SA_AUTO = 0
 DSA_SA_MULTIPLICITY = 1
@@ -42,6 +42,7 @@ EXPORTS = (
     "dsa_indexer_q_proj",
     "dsa_indexer_pack_projection_weights",
     "dsa_indexer_projections",
+    "dsa_indexer_decode_projections",
 )
 
 _c_i64 = ctypes.c_int64
@@ -133,6 +134,9 @@ def load() -> ctypes.CDLL:
     lib.dsa_indexer_projections.argtypes = [
         _c_vp, _c_vp, _c_vp, ctypes.c_int32, _c_vp, _c_vp, _c_vp, _c_vp,
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]
+    lib.dsa_indexer_decode_projections.restype = ctypes.c_int
+    lib.dsa_indexer_decode_projections.argtypes = [
+        _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]
     v = lib.dsa_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {v}, expected {ABI_VERSION}")
@@ -172,8 +176,20 @@ class Launch:
 
     def __init__(self, name: str, args: list):
         self.name = name
-        self.fn = getattr(load(), name)
-        self.args = args
+        lib = load()
+        # The arguments are converted to ctypes objects once, by the entry point's declared
+        # types; each call passes them to an untyped handle of the same symbol, which skips the
+        # per-call conversion (about a third of a 14-argument call's cost).
+        types = getattr(lib, name).argtypes
+        if len(types) != len(args):
+            raise TypeError(f"{name}: {len(args)} arguments for {len(types)} parameters")
+        self.fn = lib[name]
+        self.fn.restype = ctypes.c_int
+        self.args = [t(a) for t, a in zip(types, args)]
+
+    def set(self, slot: int, ptr: int) -> None:
+        """Patch a pointer argument (a fresh output)."""
+        self.args[slot].value = ptr
 
     def __call__(self) -> None:
         rc = self.fn(*self.args)
@@ -196,20 +212,35 @@ class Prepared:
     """A checked, marshalled call and what it needs kept alive (inputs made contiguous,
     workspaces, the fp32 sink copy). run() allocates the fresh output, patches its pointer
     into the argument slot `out_slot` and launches."""
-    __slots__ = ("launch", "out_slot", "out_shape", "out_dtype", "device", "keep")
+    __slots__ = ("launch", "out_slot", "out_shape", "out_dtype", "device", "keep", "_like", "_proto")
 
     def __init__(self, launch: Launch, out_slot: int, out_shape, out_dtype, device, keep):
         self.launch = launch
         self.out_slot = out_slot
-        self.out_shape = out_shape
+        self.out_shape = tuple(out_shape)
         self.out_dtype = out_dtype
         self.device = device
         self.keep = keep
+        # The output is allocated from the first kept input (a device tensor): empty_like when
+        # it has the output's shape and dtype, else new_empty; both parse fewer arguments than
+        # torch.empty(..., device=...), a measurable part of a steady-state call.
+        proto = keep[0] if keep and isinstance(keep[0], torch.Tensor) and keep[0].device == device else None
+        self._like = proto if (proto is not None and tuple(proto.shape) == self.out_shape
+                               and proto.dtype == out_dtype and proto.is_contiguous()) else None
+        self._proto = proto
 
     def run(self) -> torch.Tensor:
-        out = torch.empty(self.out_shape, dtype=self.out_dtype, device=self.device)
-        self.launch.args[self.out_slot] = out.data_ptr()
-        self.launch()
+        if self._like is not None:
+            out = torch.empty_like(self._like)
+        elif self._proto is not None:
+            out = self._proto.new_empty(self.out_shape, dtype=self.out_dtype)
+        else:
+            out = torch.empty(self.out_shape, dtype=self.out_dtype, device=self.device)
+        launch = self.launch
+        launch.args[self.out_slot].value = out.data_ptr()
+        rc = launch.fn(*launch.args)
+        if rc != 0:
+            _check(launch.name, rc)
         return out
 
 
@@ -500,7 +531,47 @@ def indexer_projections(qr: torch.Tensor, wq_packed: torch.Tensor, freqs_cis: Op
                                                                    head_dim, rope_head_dim, rope_mode)
     q = torch.empty(q_shape, dtype=torch.bfloat16, device=qr.device)
     wl = torch.empty(wl_shape, dtype=torch.bfloat16, device=qr.device)
-    launch.args[PROJ_SLOT_Q] = q.data_ptr()
-    launch.args[PROJ_SLOT_WL] = wl.data_ptr()
+    launch.set(PROJ_SLOT_Q, q.data_ptr())
+    launch.set(PROJ_SLOT_WL, wl.data_ptr())
+    launch()
+    return q, wl
+
+
+#: argument slots of the two outputs of dsa_indexer_decode_projections
+DECODE_SLOT_Q = 4
+DECODE_SLOT_WL = 5
+
+
+def prepare_indexer_decode_projections(qr: torch.Tensor, wq: torch.Tensor, x: torch.Tensor, wproj: torch.Tensor):
+    """Checks and marshals dsa_indexer_decode_projections; returns (Launch, q_shape,
+    wl_shape, keep) with the outputs in the argument slots DECODE_SLOT_Q / DECODE_SLOT_WL.
+    qr: bf16 [b, s, 1536], x: bf16 [b, s, 7168] with b * s <= 16; wq [n_q, 1536] and
+    wproj [n_w, 7168] the Linear weights as they are."""
+    load()
+    if qr.dim() != 3 or x.dim() != 3 or qr.shape[:2] != x.shape[:2]:
+        raise ValueError(f"qr {tuple(qr.shape)} and x {tuple(x.shape)} do not match")
+    if wq.dim() != 2 or wproj.dim() != 2 or wq.shape[1] != qr.shape[2] or wproj.shape[1] != x.shape[2]:
+        raise ValueError(f"weights {tuple(wq.shape)} / {tuple(wproj.shape)} do not match qr / x")
+    for t in (qr, x, wq, wproj):
+        if t.dtype != torch.bfloat16:
+            raise TypeError("qr, x and both weights must be bfloat16")
+    b, s, k_q = qr.shape
+    k_w = x.shape[2]
+    qr, x, wq, wproj = qr.contiguous(), x.contiguous(), wq.contiguous(), wproj.contiguous()
+    dev = _require_gpu(qr, x, wq, wproj)
+    args = [qr.data_ptr(), wq.data_ptr(), x.data_ptr(), wproj.data_ptr(), None, None,
+            b * s, wq.shape[0], k_q, wproj.shape[0], k_w, stream_handle(dev)]
+    return (Launch("dsa_indexer_decode_projections", args), (b, s, wq.shape[0]), (b, s, wproj.shape[0]),
+            (qr, x, wq, wproj))
+
+
+def indexer_decode_projections(qr: torch.Tensor, wq: torch.Tensor, x: torch.Tensor, wproj: torch.Tensor):
+    """q = qr . wq^T as bf16 [b, s, n_q] and wl = x . wproj^T as bf16 [b, s, n_w] for
+    b * s <= 16 tokens, in hipBLASLt's local-split rounding (no RoPE)."""
+    launch, q_shape, wl_shape, _keep = prepare_indexer_decode_projections(qr, wq, x, wproj)
+    q = torch.empty(q_shape, dtype=torch.bfloat16, device=qr.device)
+    wl = torch.empty(wl_shape, dtype=torch.bfloat16, device=qr.device)
+    launch.set(DECODE_SLOT_Q, q.data_ptr())
+    launch.set(DECODE_SLOT_WL, wl.data_ptr())
     launch()
     return q, wl

@@ -11,10 +11,12 @@ so a seeded construction yields the reference's weights.
 forward = the two projections, then one gfx950 kernel for the score, the
 relu-weighted head sum, the causal mask and the top-k (``dsa_indexer_score_topk``).
 The projections run as one kernel launch (``dsa_indexer_projections``: q with RoPE,
-and the head weights), as the query-projection kernel beside ``F.linear``, or as two
-``F.linear`` (the reference's own op; the score kernel then applies RoPE), whichever
-``projection_route`` picks: a kernel only where its rounding was measured equal to
-``F.linear`` on this torch-ROCm build. Inputs must be on the HIP device;
+and the head weights), as the query-projection kernel beside ``F.linear``, as one
+decode launch for 1..16 tokens (``dsa_indexer_decode_projections``, both products in
+hipBLASLt's split-k order; the score kernel applies RoPE), or as two ``F.linear`` (the
+reference's own op; the score kernel then applies RoPE), whichever ``projection_route``
+picks: a kernel only where its rounding was measured equal to ``F.linear`` on this
+torch-ROCm build. Inputs must be on the HIP device;
 unsupported configurations raise.
 """
 from __future__ import annotations
@@ -145,6 +147,12 @@ WL_EQUAL = (
 #: smallest token count sent to the query-projection kernel (below it F.linear + the score
 #: kernel's own RoPE is as fast)
 Q_PROJ_MIN_TOKENS = 64
+#: Decode (1..16 tokens) at the DeepSeek-V3.2 sizes (q_lora_rank, n_heads * head_dim, dim,
+#: n_heads): there hipBLASLt runs both products with k split over 4 waves, the order
+#: dsa_indexer_decode_projections reproduces (measured for every token count 1..16 on that
+#: build, tests/test_gpu_decode_proj.py).
+DECODE_MAX_TOKENS = 16
+DECODE_SHAPE = (1536, 8192, 7168, 64)
 
 _build_ok: dict = {}
 
@@ -168,10 +176,14 @@ def projection_route(m: int, q_lora_rank: int, rope_head_dim: int, head_dim: int
     """Which path computes the two projections of Model.forward for m = b * s tokens:
     'both'  one launch of dsa_indexer_projections (q with RoPE, and weights_proj);
     'q'     dsa_indexer_q_proj for q with RoPE, F.linear for weights_proj;
+    'decode' one launch of dsa_indexer_decode_projections for both (no RoPE: the score
+            kernel applies it);
     'torch' F.linear for both (the score kernel then applies RoPE).
     A kernel is used only where its rounding was measured equal to F.linear."""
     if not (bf16 and on_gpu and build_ok):
         return "torch"
+    if 1 <= m <= DECODE_MAX_TOKENS and (q_lora_rank, n_q, dim, n_w) == DECODE_SHAPE:
+        return "decode"
     if not (q_lora_rank == 256 and rope_head_dim == 32 and n_q % 256 == 0 and head_dim in (64, 128)
             and m >= Q_PROJ_MIN_TOKENS and _within(m, Q_EQUAL)):
         return "torch"
@@ -210,7 +222,7 @@ class Model(nn.Module):
         self._packed = None
 
     def route(self, x: torch.Tensor, qr: torch.Tensor) -> str:
-        """projection_route for these inputs ('both', 'q' or 'torch')."""
+        """projection_route for these inputs ('both', 'q', 'decode' or 'torch')."""
         wq, wp = self.wq_b.weight, self.weights_proj.weight
         return projection_route(
             qr.shape[0] * qr.shape[1], qr.shape[-1], self.rope_head_dim, self.head_dim, wq.shape[0], x.shape[-1],
@@ -260,7 +272,7 @@ class Model(nn.Module):
         return projection_route(
             qr.shape[0] * qr.shape[1], qr.shape[-1], self.rope_head_dim, self.head_dim, wq.shape[0], self.dim,
             wp.shape[0], qr.dtype == wq.dtype == torch.bfloat16, qr.is_cuda,
-            qr.is_cuda and _measured_build(qr.device)) != "torch"
+            qr.is_cuda and _measured_build(qr.device)) in ("both", "q")
 
 
 class _IndexerPlan:
@@ -298,14 +310,24 @@ class _IndexerPlan:
                 qr, wq_p, freqs, x, wp_p, hd, rd, mode)
             self.q = torch.empty(q_shape, dtype=torch.bfloat16, device=x.device)
             self.wl = torch.empty(wl_shape, dtype=torch.bfloat16, device=x.device)
-            self.proj.args[_native.PROJ_SLOT_Q] = self.q.data_ptr()
-            self.proj.args[_native.PROJ_SLOT_WL] = self.wl.data_ptr()
+            self.proj.set(_native.PROJ_SLOT_Q, self.q.data_ptr())
+            self.proj.set(_native.PROJ_SLOT_WL, self.wl.data_ptr())
             self.score = _native.prepare_indexer_score_topk(self.q, kv, self.wl, w_scale, None, **score_kw)
+        elif self.route == "decode":
+            # q = qr . wq_b^T and wl = x . weights_proj^T in one launch, in hipBLASLt's
+            # rounding at decode sizes (task2_v0_ref.py:129,132); RoPE in the score kernel.
+            self.proj, _q_shape, wl_shape, self.proj_keep = _native.prepare_indexer_decode_projections(
+                qr, self.wq, x, self.wp)
+            self.q = torch.empty(bsz, seqlen, model.n_local_heads, hd, dtype=torch.bfloat16, device=x.device)
+            self.wl = torch.empty(wl_shape, dtype=torch.bfloat16, device=x.device)
+            self.proj.set(_native.DECODE_SLOT_Q, self.q.data_ptr())
+            self.proj.set(_native.DECODE_SLOT_WL, self.wl.data_ptr())
+            self.score = _native.prepare_indexer_score_topk(self.q, kv, self.wl, w_scale, freqs, **score_kw)
         elif self.route == "q":
             # q = RoPE(qr . wq_b^T) by dsa_indexer_q_proj; weights_proj stays F.linear.
             prep = _native.prepare_indexer_q_proj(qr, self.wq, freqs, hd, rd, mode)
             self.q = torch.empty(prep.out_shape, dtype=torch.bfloat16, device=x.device)
-            prep.launch.args[prep.out_slot] = self.q.data_ptr()
+            prep.launch.set(prep.out_slot, self.q.data_ptr())
             self.proj, self.proj_keep = prep.launch, prep.keep
             wl0 = torch.empty(bsz, seqlen, model.n_heads, dtype=torch.bfloat16, device=x.device)
             self.score = _native.prepare_indexer_score_topk(self.q, kv, wl0, w_scale, None, **score_kw)
@@ -319,18 +341,18 @@ class _IndexerPlan:
     def run(self) -> torch.Tensor:
         if self.empty is not None:
             return torch.empty(*self.empty, 0, dtype=torch.int64, device=self.device)
-        args = self.score.launch.args
-        if self.route == "both":
+        launch = self.score.launch
+        if self.route == "both" or self.route == "decode":
             self.proj()
         elif self.route == "q":
             self.proj()
             wl = F.linear(self.x, self.wp)
-            args[_native.SCORE_SLOT_WL] = wl.data_ptr()
+            launch.set(_native.SCORE_SLOT_WL, wl.data_ptr())
         else:
             q = F.linear(self.qr, self.wq).unflatten(-1, self.heads)
             wl = F.linear(self.x, self.wp)
-            args[_native.SCORE_SLOT_Q] = q.data_ptr()
-            args[_native.SCORE_SLOT_WL] = wl.data_ptr()
+            launch.set(_native.SCORE_SLOT_Q, q.data_ptr())
+            launch.set(_native.SCORE_SLOT_WL, wl.data_ptr())
         # (The fresh q / wl tensors of the torch paths are released when this returns; the
         # caching allocator hands their memory only to later work on this stream.)
         return self.score.run()

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 3
+#define DSA_ABI_VERSION 4
 
 #define DSA_OK 0
 #define DSA_ERR_NULL (-1)        /* a required pointer is NULL */
@@ -333,6 +333,24 @@ int dsa_indexer_projections(const void* qr, const void* wq_packed, const void* f
                             int32_t rope_mode, void* q, const void* x, const void* wproj_packed,
                             void* wl, int64_t m, int64_t n, int64_t k, int64_t dim, int64_t n_w,
                             int64_t head_dim, int64_t rd, int64_t s_len, void* stream);
+
+/*
+ * The indexer's two projections for a few tokens (decode), in one launch, without RoPE
+ * (the score kernel applies it): the F.linear calls of reference/task2_v0_ref.py:129
+ * (q = qr . wq^T) and :132 (wl = x . wproj^T), Linear.forward :81-83. At the DeepSeek-V3.2
+ * sizes (q_lora_rank 1536, dim 7168) and 1..16 tokens, torch-ROCm's hipBLASLt splits k
+ * over 4 waves: in every depth block of 128 (q) or 512 (wl), chain c accumulates the
+ * c-th quarter in fp32 in ascending k over all blocks, and the four chains are summed as
+ * ((c0 + c1) + c2) + c3 and rounded once to bf16. This entry point computes exactly that
+ * sum (bit-equal to F.linear on the build the drop-in Model gates it on).
+ *   qr     bf16 [m, k_q], k_q == 1536          wq     bf16 [n_q, k_q] (wq_b.weight), n_q % 64 == 0
+ *   x      bf16 [m, k_w], k_w == 7168          wproj  bf16 [n_w, k_w] (weights_proj.weight), n_w % 16 == 0
+ *   q      bf16 [m, n_q] output                wl     bf16 [m, n_w] output (both 2-byte aligned)
+ * 0 <= m <= 16, n_q % 64 == 0; inputs 16-byte aligned, rows contiguous.
+ */
+int dsa_indexer_decode_projections(const void* qr, const void* wq, const void* x, const void* wproj,
+                                   void* q, void* wl, int64_t m, int64_t n_q, int64_t k_q, int64_t n_w,
+                                   int64_t k_w, void* stream);
 
 #ifdef __cplusplus
 }

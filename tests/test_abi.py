@@ -294,3 +294,24 @@ def test_pack_projection_weights_host_checks():
     assert f(None, 0, 0, 16, 20, 1024, None, 16, None) == -3         # n_w % 16
     assert f(None, 0, 0, 16, 16, 1000, None, 16, None) == -3         # dim % 32
     assert f(8, 1024, 256, None, 0, 0, 16, None, None) == -6
+
+
+def _dproj(lib, m=1, n_q=8192, k_q=1536, n_w=64, k_w=7168, **ptrs):
+    p = dict(qr=16, wq=16, x=16, wp=16, q=16, wl=16)
+    p.update(ptrs)
+    return lib.dsa_indexer_decode_projections(p["qr"], p["wq"], p["x"], p["wp"], p["q"], p["wl"],
+                                              m, n_q, k_q, n_w, k_w, None)
+
+
+def test_decode_projections_host_checks():
+    """Shape, pointer and alignment errors of dsa_indexer_decode_projections come back before
+    anything is launched (no GPU needed)."""
+    lib = _native.load()
+    assert _dproj(lib, m=-1) == -2 and _dproj(lib, n_q=0) == -2 and _dproj(lib, k_w=-5) == -2
+    assert _dproj(lib, m=17) == -3                  # 1..16 tokens
+    assert _dproj(lib, k_q=1024) == -3 and _dproj(lib, k_w=4096) == -3   # the measured depths only
+    assert _dproj(lib, n_q=8160) == -3 and _dproj(lib, n_w=40) == -3     # 64-channel / 16-channel tiles
+    assert _dproj(lib, m=0) == 0                    # nothing to do
+    for name in ("qr", "wq", "x", "wp", "q", "wl"):
+        assert _dproj(lib, **{name: None}) == -1, name
+    assert _dproj(lib, qr=8) == -6 and _dproj(lib, wp=24) == -6 and _dproj(lib, q=17) == -6

@@ -122,7 +122,20 @@ def test_projection_route_boundaries():
     assert r(8 * 2600, dim=2048) == r(8 * 2600, n_w=32) == "q"
     assert r(8 * 2600, head_dim=128) == "q"            # the one-launch kernel is head_dim 64 only
     assert r(8 * 2600, q_lora_rank=1536) == r(8 * 2600, rope_head_dim=64) == "torch"   # configs[4]
-    assert r(1) == "torch"                             # decode
+    assert r(1) == "torch"                             # decode at the configs[2] sizes
+
+
+def test_projection_route_decode():
+    """1..16 tokens at the configs[4] sizes (q_lora_rank 1536, 64 x 128 query channels, dim
+    7168, 64 head weights) take the decode launch, on the measured build only; any other
+    size or count keeps F.linear."""
+    c5 = dict(q_lora_rank=1536, rope_head_dim=64, head_dim=128, n_q=8192, dim=7168, n_w=64, bf16=True,
+              on_gpu=True, build_ok=True)
+    r = lambda m, **kw: t2.projection_route(m, **{**c5, **kw})
+    assert [r(m) for m in range(1, 17)] == ["decode"] * 16
+    assert r(0) == r(17) == r(8192) == "torch"
+    assert r(1, build_ok=False) == r(1, on_gpu=False) == r(1, bf16=False) == "torch"
+    assert r(1, n_q=4096) == r(1, dim=4096) == r(1, n_w=32) == r(1, q_lora_rank=1024) == "torch"
 
 
 def test_projection_tables_match_measurement():
