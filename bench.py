@@ -355,6 +355,11 @@ def main():
             _warm(torch, stepd, 2, 0.05)
             ms_de = _events_time(torch, stepd, nd, stream)
             eq = bool(torch.equal(outd.view(torch.int16), stepd().view(torch.int16)))
+            # the indexer's projections alone (its cached launch: both products in one
+            # kernel when the route is 'decode')
+            pl = ixd._plan
+            route_d = pl.route if pl is not None else None
+            ms_dp = _events_time(torch, pl.proj, nd, stream) if route_d == "decode" else None
         dsa_decode = {
             "workload": "configs[4] decode: 1 new token at position 8191 of 8192; indexer 64x128 (qr[1,1,1536], "
                         "x[1,1,7168], kv_cache[1,8192,128], top-2048, no mask) then sparse MLA q[1,1,128,576] over "
@@ -362,6 +367,9 @@ def main():
             "graph_us_per_step": round(ms_dg * 1e3, 1),
             "eager_us_per_step": round(ms_de * 1e3, 1),
             "graph_replay_equals_eager": eq,
+            "projection_route": route_d,
+            "projections_us": round(ms_dp * 1e3, 2) if ms_dp is not None else None,
+            "projections_bytes": 26117248,
         }
         del graph, outd, xd, qrd, qd, kvd, ixd, mlad
         torch.cuda.empty_cache()
