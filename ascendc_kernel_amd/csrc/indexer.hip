@@ -18,7 +18,7 @@
 //
 // One wave owns two consecutive tokens of one batch. Their 2 x 16 head rows
 // form the A operand of v_mfma_f32_32x32x16_bf16 against 32 candidate keys per
-// tile; v_permlane32_swap then gives every lane all 16 head scores of one
+// tile, in a row order that leaves every lane all 16 head scores of one
 // (token, candidate), so the epilogue and the head sum are lane-local. Scores
 // become 16-bit order keys in LDS; a two-pass 8-bit radix select per half-wave
 // finds the k-th key, ties are taken in index order with ballots, and the k
@@ -28,6 +28,7 @@
 #include "dsa_common.h"
 
 #include <atomic>
+#include <type_traits>
 #include <mutex>
 
 using namespace dsa;
@@ -200,12 +201,16 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
     for (int i = 0; i < kH; ++i) w[i] = 0.f;
   }
 
-  // A operand: row i = lane % 32 is (token t0 + i/16, head i%16); lane holds
-  // channels 16ks + 8(lane/32) .. +7 of that row, RoPE applied when asked.
+  // A operand: row i = lane % 32 is token t0 + (i/4)%2, head i%4 + 4(i/8); lane
+  // holds channels 16ks + 8(lane/32) .. +7 of that row, RoPE applied when asked.
+  // The 32x32 product leaves rows 8(r/4) + 4(lane/32) + r%4 in accumulator r of a
+  // lane, so with this row order accumulator r of lanes 0..31 is head r of token t0
+  // and of lanes 32..63 head r of token t0 + 1, for candidate lane % 32: every lane
+  // holds all 16 heads of one (token, candidate) without an exchange of halves.
   bf16x8 qa[4];
   {
-    const int tq = t0 + ((lane & 31) >> 4);
-    const int hq = lane & 15;
+    const int tq = t0 + ((lane >> 2) & 1);
+    const int hq = (lane & 3) | (((lane & 31) >> 3) << 2);
     const int hsel = lane >> 5;
     if (tq < p.S) {
       const int64_t row = ((int64_t)b * p.S + tq) * kH + hq;
@@ -266,37 +271,32 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
   // B operand: candidate 32*tile + lane%32, channels 16ks + 8(lane/32) .. +7.
   const int kcol = lane & 31;
   const int khalf = lane >> 5;
-  int slot = 0;  // tile % 3
-  for (int tile = 0; tile < ntile; ++tile) {
+  // Lane offsets of the four B fragments inside a ring slot (the slot is a constant in
+  // each unrolled step below, so it becomes the LDS instructions' immediate offset).
+  uint32_t boff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    boff[ks] = ring_lds + 16u * (uint32_t)(8 * kcol + ((2 * ks + khalf) ^ (kcol & 7)));
+  auto step = [&](auto slot_c, const int tile) {
+    constexpr int kSlot = decltype(slot_c)::value;  // tile % 3
     if (tile + 1 < ntile) wait_vmcnt<1>();
     else wait_vmcnt<0>();
     __syncthreads();  // tile `tile` is in LDS for every wave; the slot of tile-1 is free
-    const int slot_next = slot == 0 ? 2 : slot - 1;  // (tile + 2) % 3 == (tile - 1) % 3
-    if (tile + 2 < ntile) issue(tile + 2, slot_next);
-    const u32x4* kt = reinterpret_cast<const u32x4*>(ring + 4096 * slot);
-    slot = slot == 2 ? 0 : slot + 1;
+    if (tile + 2 < ntile) issue(tile + 2, (kSlot + 2) % 3);  // (tile + 2) % 3 == (tile - 1) % 3
     f32x16 acc = {};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      acc = mfma32x32x16(qa[ks], __builtin_bit_cast(bf16x8, kt[8 * kcol + ((2 * ks + khalf) ^ (kcol & 7))]), acc);
+    for (int ks = 0; ks < 4; ++ks) {
+      const auto* src = (__attribute__((address_space(3))) const u32x4*)(uintptr_t)(boff[ks] + 4096u * kSlot);
+      acc = mfma32x32x16(qa[ks], __builtin_bit_cast(bf16x8, *src), acc);
+    }
 
     // The einsum's bf16 rounding, then relu on the bf16 bit patterns (both heads
-    // of a word at once): word k holds slots 2k, 2k+1.
+    // of a word at once): word k holds heads 2k, 2k+1.
     uint32_t pk[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       s16v2 h = __builtin_bit_cast(s16v2, pack_bf2(acc[2 * k], acc[2 * k + 1]));
       pk[k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(h, (s16v2){0, 0}));
-    }
-    // Exchange halves: afterwards lanes 0..31 hold token t0, lanes 32..63 token
-    // t0+1, all 16 heads of candidate 32*tile + lane%32. Slot r holds head
-    // r (r<4), r+4 (4<=r<8), r-4 (8<=r<12), r (12<=r). (The swap operands are
-    // computed words, never raw accumulator elements.)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(pk[k], pk[k + 4], false, false);
-      pk[k] = (uint32_t)sw[0];
-      pk[k + 4] = (uint32_t)sw[1];
     }
     // * w -> bf16 (the products are exact in fp32), as fp32 values: one
     // v_cvt_pk_bf16_f32 with a zero low operand leaves bf16(x) in the high half and
@@ -304,18 +304,16 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
     float v[16];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int r = 2 * k;
-      const int h0 = (r < 4) ? r : (r < 8) ? r + 4 : (r < 12) ? r - 4 : r;
-      v[r] = bf16_as_f32(bf_lo(pk[k]) * w[h0]);
-      v[r + 1] = bf16_as_f32(bf_hi(pk[k]) * w[h0 + 1]);
+      v[2 * k] = bf16_as_f32(bf_lo(pk[k]) * w[2 * k]);
+      v[2 * k + 1] = bf16_as_f32(bf_hi(pk[k]) * w[2 * k + 1]);
     }
-    // Head j is in slot j (j<4), j+4 -> slot j+8, j+8 -> slot j+4, j+12 -> slot j+12;
-    // IEEE fp32 adds in torch's order. torch's four accumulators start at +0; adding
-    // the +0 once to the total instead gives the same value (x + 0 == x except for
-    // the sign of a zero, and a -0 can only reach the total when every term is -0).
+    // IEEE fp32 adds in torch's order (accumulator j sums heads j, j+4, j+8, j+12).
+    // torch's four accumulators start at +0; adding the +0 once to the total instead
+    // gives the same value (x + 0 == x except for the sign of a zero, and a -0 can
+    // only reach the total when every term is -0).
     float a4[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a4[j] = ((v[j] + v[j + 8]) + v[j + 4]) + v[j + 12];
+    for (int j = 0; j < 4; ++j) a4[j] = ((v[j] + v[j + 4]) + v[j + 8]) + v[j + 12];
     const float tot = (((a4[0] + a4[1]) + a4[2]) + a4[3]) + 0.0f;
     uint16_t sc = f2bf(tot);
     const int c = 32 * tile + hl;
@@ -330,6 +328,11 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
         p.scores[((int64_t)b * p.S + t) * p.T + c] = valid ? sc : (uint16_t)0xff80u;
     }
     if (valid) atomicAdd(&myhist[u >> 8], 1u);
+  };
+  for (int tile0 = 0; tile0 < ntile; tile0 += 3) {
+    step(std::integral_constant<int, 0>{}, tile0);
+    if (tile0 + 1 < ntile) step(std::integral_constant<int, 1>{}, tile0 + 1);
+    if (tile0 + 2 < ntile) step(std::integral_constant<int, 2>{}, tile0 + 2);
   }
   if constexpr (kDump) {  // score dump only: fill the never-valid tail with -inf
     if (t < p.S)

@@ -306,6 +306,57 @@ def test_score_stage_matches_torch(gpu, seqlen, start_pos):
     assert not bad.any(), int(bad.sum())
 
 
+@pytest.mark.parametrize("start_pos,seqlen,k", [(2536, 64, 128), (2536, 64, 32), (0, 2600, 128)])
+def test_score_stage_nonfinite(gpu, start_pos, seqlen, k):
+    """Scores that overflow to +-inf (about a quarter of the candidates carry an inf head):
+    the kernel's bf16 score and its top-k equal torch's on the same GPU. With the causal
+    mask (start_pos 0) only the unmasked scores are compared: the reference adds -inf to
+    a masked +inf score, which gives NaN and ranks that masked candidate first (then
+    filled with -1); the kernel counts masked candidates as -inf without scoring them, so
+    its picks differ from the reference's on such rows. NaN scores are not covered: the
+    kernel's packed relu maps a NaN with the sign bit set (the matrix cores' NaN) to 0
+    where torch.relu keeps it."""
+    args = t2._make_args()
+    m, r = _pair(args, 31, 2, 650, gpu)
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(2, seqlen, 1024, generator=g).to(torch.bfloat16).to(gpu)
+    qr = torch.randn(2, seqlen, 256, generator=g).to(torch.bfloat16).to(gpu)
+    wq = m.wq_b.weight.detach().clone()
+    # channel 0 of heads 3 and 10 becomes -+3e38 on even tokens (rope leaves channel 0
+    # alone), so q . k overflows to +-inf wherever |k_0| > ~1.13
+    wq[3 * 64, 0] = 1e19
+    wq[10 * 64, 0] = -1e19
+    qr[:, 0::2, 0] = 3e19
+    kv = m.kv_cache.detach().clone()
+    end = start_pos + seqlen
+    n_cand = end // 4
+    causal = start_pos == 0
+    _say("score stage non-finite", start_pos, seqlen, k)
+    want = oix.index_scores(wq, m.weights_proj.weight, kv, m.freqs_cis, x, qr, start_pos, 16, 64, 32, 4)
+    q = torch.nn.functional.linear(qr, wq).unflatten(-1, (16, 64)).contiguous()
+    wl = torch.nn.functional.linear(x, m.weights_proj.weight)
+    scale = 64 ** -0.5 * 16 ** -0.5
+    fr = m.freqs_cis[start_pos:end]
+    got = _native.indexer_scores(q, kv, wl, scale, fr, 32, n_cand, 4, causal)
+    gb, wb = bits_of(got).reshape(-1, n_cand), bits_of(want).reshape(-1, n_cand)
+    t = np.tile(np.arange(seqlen), 2)
+    n_r = np.minimum((t + 1) // 4, n_cand) if causal else np.full(t.shape, n_cand)
+    valid = np.arange(n_cand)[None, :] < n_r[:, None]
+    g_nan = (gb & 0x7FFF) > 0x7F80
+    w_nan = (wb & 0x7FFF) > 0x7F80
+    n_inf = int((((wb & 0x7FFF) == 0x7F80) & valid).sum())
+    _say(f"inf scores {n_inf}, NaN scores {int((w_nan & valid).sum())} of {int(valid.sum())}")
+    assert n_inf > 1000 and not (w_nan & valid).any()
+    same = (gb == wb) | (g_nan & w_nan)
+    assert same[valid].all(), int((~same[valid]).sum())
+    if causal:
+        return
+    idx = _native.indexer_score_topk(q, kv, wl, scale, fr, 32, n_cand, k, 4, False, 0).cpu().numpy()
+    want_idx = oix.select_topk(want, start_pos, 0, k, 4).cpu().numpy()  # torch.topk on this GPU
+    bad = (idx.reshape(-1, k) != want_idx.reshape(-1, k)).any(axis=1)
+    assert not bad.any(), int(bad.sum())
+
+
 def test_model_launch_plan_reuse(gpu):
     """Model.forward's cached plan (one launch of both projections at configs[2]): repeated
     calls agree and return fresh tensors; new inputs, new input contents under the same
