@@ -29,6 +29,11 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
 }
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+// bf16(x) (round to nearest even) as an fp32 value: one v_cvt_pk_bf16_f32 with a zero
+// low operand leaves bf16(x) in the high half and zeros below it. Cheaper than a
+// packed conversion of two values followed by the two extractions (the low half needs
+// a left shift, which issues at the slower of the gfx950 VALU rates).
+__device__ __forceinline__ float bf16_as_f32(float x) { return __builtin_bit_cast(float, pack_bf2(0.f, x)); }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

@@ -109,9 +109,6 @@ __device__ __forceinline__ uint32_t xor_lanes(uint32_t v, int m) {
   return (uint32_t)__builtin_amdgcn_ds_swizzle(x, (16 << 10) | 0x1F);
 }
 
-// bf16(x) (round to nearest even) as an fp32 value, one v_cvt_pk_bf16_f32.
-__device__ __forceinline__ float bf16_as_f32(float x) { return __builtin_bit_cast(float, pack_bf2(0.f, x)); }
-
 __device__ __forceinline__ void lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
 // Per half-wave: the bin b of a 256-bin histogram (bins ascending in key) with

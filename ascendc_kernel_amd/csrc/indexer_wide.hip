@@ -551,16 +551,17 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
       // bf16 x bf16 products are exact in fp32; each is rounded to bf16 and added
       // with an IEEE fp32 add (v_dot2c's accumulation does not always round like one).
       const uint32_t pv = __builtin_bit_cast(uint32_t, pk);
-      const uint32_t pp = pack_bf2(bf_lo(pv) * bf_lo(wlo[m]), bf_hi(pv) * bf_hi(whi[m]));
+      const float p0 = bf16_as_f32(bf_lo(pv) * bf_lo(wlo[m]));
+      const float p1 = bf16_as_f32(bf_hi(pv) * bf_hi(whi[m]));
       if constexpr (KY == 2) {
-        acc[0] = acc[0] + bf_lo(pp);
-        acc[1] = acc[1] + bf_hi(pp);
+        acc[0] = acc[0] + p0;
+        acc[1] = acc[1] + p1;
       } else if constexpr (KY == 4) {
-        acc[2 * (m & 1)] = acc[2 * (m & 1)] + bf_lo(pp);
-        acc[2 * (m & 1) + 1] = acc[2 * (m & 1) + 1] + bf_hi(pp);
+        acc[2 * (m & 1)] = acc[2 * (m & 1)] + p0;
+        acc[2 * (m & 1) + 1] = acc[2 * (m & 1) + 1] + p1;
       } else {
-        acc[0] = acc[0] + bf_lo(pp);
-        acc[0] = acc[0] + bf_hi(pp);
+        acc[0] = acc[0] + p0;
+        acc[0] = acc[0] + p1;
       }
     }
     float ty;
