@@ -274,6 +274,8 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
     boff[ks] = ring_lds + 16u * (uint32_t)(8 * kcol + ((2 * ks + khalf) ^ (kcol & 7)));
+  // The smaller of the two tokens' valid candidate counts (wave-uniform).
+  const int nv_min = min(__builtin_amdgcn_readfirstlane(nv), __builtin_amdgcn_readlane(nv, 32));
   auto step = [&](auto slot_c, const int tile) {
     constexpr int kSlot = decltype(slot_c)::value;  // tile % 3
     if (tile + 1 < ntile) wait_vmcnt<1>();
@@ -312,19 +314,29 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) a4[j] = ((v[j] + v[j + 4]) + v[j + 8]) + v[j + 12];
     const float tot = (((a4[0] + a4[1]) + a4[2]) + a4[3]) + 0.0f;
-    uint16_t sc = f2bf(tot);
+    // The reference adds the 0/-inf mask, bf16(x + 0), which only turns -0 into +0.
+    // Here sc is never -0: tot is +0 (the + 0 above) or a sum of bf16 values, all
+    // multiples of 2^-133, so |tot| >= 2^-133 rounds to a nonzero bf16 (the conversion
+    // keeps fp32 denormals: it matches IEEE round-to-nearest-even on them).
+    const uint16_t sc = f2bf(tot);
     const int c = 32 * tile + hl;
     const bool valid = c < nv;
-    // The reference adds the 0/-inf mask: bf16(x + 0) turns -0 into +0, nothing else.
-    if (p.causal && sc == 0x8000u) sc = 0;
-    uint16_t u = (uint16_t)(sc ^ ((sc & 0x8000u) ? 0xffffu : 0x8000u));
+    // Order key: sign set -> all bits flipped, else the sign bit flipped; the sign of
+    // the bf16 is that of tot (NaN aside), taken from tot's bits with one shift.
+    const uint32_t neg = (uint32_t)((int32_t)__builtin_bit_cast(uint32_t, tot) >> 31);
+    uint16_t u = (uint16_t)(sc ^ (neg | 0x8000u));
     if (__builtin_isnan(tot)) u = 0xffffu;  // NaN ranks above everything
-    keys[(half * ntile_all + tile) * 32 + hl] = valid ? u : (uint16_t)0;
     if constexpr (kDump) {
       if (t < p.S && c < p.T)
         p.scores[((int64_t)b * p.S + t) * p.T + c] = valid ? sc : (uint16_t)0xff80u;
     }
-    if (valid) atomicAdd(&myhist[u >> 8], 1u);
+    if (32 * tile + 32 <= nv_min) {  // (wave-uniform) every lane's candidate is valid
+      keys[(half * ntile_all + tile) * 32 + hl] = u;
+      atomicAdd(&myhist[u >> 8], 1u);
+    } else {
+      keys[(half * ntile_all + tile) * 32 + hl] = valid ? u : (uint16_t)0;
+      if (valid) atomicAdd(&myhist[u >> 8], 1u);
+    }
   };
   for (int tile0 = 0; tile0 < ntile; tile0 += 3) {
     step(std::integral_constant<int, 0>{}, tile0);
