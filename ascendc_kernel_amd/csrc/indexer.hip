@@ -406,52 +406,51 @@ __global__ __launch_bounds__(256) void ix_score_topk_kernel(IxParams p) {
     }
     return (u << 16) | (0xffffu - c);
   };
-  uint32_t gt_run = 0, eq_run = 0;
-  for (int tile0 = 0; tile0 < ntile; tile0 += 4) {
-    uint32_t u4[4];
+  // One token at a time over all 64 lanes (64 candidates a step), so the ranks come
+  // straight from the 64-bit ballots: mbcnt gives the lanes below, and the running
+  // counts stay wave-uniform.
+  uint32_t* const sbuf0 = mysbuf - KP * half;  // the wave's pick buffers, token t0 first
 #pragma unroll
-    for (int j = 0; j < 4; ++j) u4[j] = keys[(half * ntile_all + tile0 + j) * 32 + hl];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tile = tile0 + j;
-      if (tile >= ntile) break;
-      const int c = 32 * tile + hl;
-      const uint32_t u = u4[j];
-      const bool valid = c < nv;
-      const bool gt = valid && u > V;
-      const bool eq = valid && u == V;
-      // Ranks within the half from the 64-bit ballot: mbcnt counts the set lanes
-      // below this one; the upper half then drops the lower half's count.
-      const uint64_t gb = __builtin_amdgcn_ballot_w64(gt);
-      const uint32_t glo = (uint32_t)gb, ghi = (uint32_t)(gb >> 32);
-      const uint32_t g_lo_cnt = (uint32_t)__builtin_popcount(glo);
-      const uint32_t g_below = __builtin_amdgcn_mbcnt_hi(ghi, __builtin_amdgcn_mbcnt_lo(glo, 0u)) -
-                               (half ? g_lo_cnt : 0u);
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t Vh = (uint32_t)__builtin_amdgcn_readlane((int)V, 32 * h);
+    const uint32_t ngt = (uint32_t)__builtin_amdgcn_readlane((int)n_gt, 32 * h);
+    const uint32_t need = (uint32_t)__builtin_amdgcn_readlane((int)need_eq, 32 * h);
+    const int nvh = __builtin_amdgcn_readlane(nv, 32 * h);
+    const uint16_t* kh = keys + h * ntile_all * 32;
+    uint32_t* sb = sbuf0 + KP * h;
+    uint32_t gt_run = 0, eq_run = 0;
+    for (int c0 = 0; c0 < nvh; c0 += 64) {
+      const int c = c0 + lane;
+      const bool valid = c < nvh;
+      const uint32_t u = valid ? (uint32_t)kh[c] : 0u;
+      const bool gt = valid && u > Vh;
+      // Lane masks straight from the compares (a ballot of a combined condition is
+      // rebuilt from a 0/1 vector value first).
+      const uint64_t vb = __builtin_amdgcn_sicmp(c, nvh, 40);           // c < nvh (signed)
+      const uint64_t gb = __builtin_amdgcn_uicmp(u, Vh, 34) & vb;       // u > Vh
       if (gt) {
-        const uint32_t pos = gt_run + g_below;
-        if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
+        const uint32_t pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(gb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)gb, gt_run));
+        if (pos < (uint32_t)KP) sb[pos] = entry(u, (uint32_t)c);
       }
-      gt_run += half ? (uint32_t)__builtin_popcount(ghi) : g_lo_cnt;
-      const uint64_t eb = __builtin_amdgcn_ballot_w64(eq);
-      if (eb != 0) {  // ties with the k-th key are rare: skip the tile otherwise
-        const uint32_t elo = (uint32_t)eb, ehi = (uint32_t)(eb >> 32);
-        const uint32_t e_lo_cnt = (uint32_t)__builtin_popcount(elo);
-        const uint32_t er = eq_run + __builtin_amdgcn_mbcnt_hi(ehi, __builtin_amdgcn_mbcnt_lo(elo, 0u)) -
-                            (half ? e_lo_cnt : 0u);
-        if (eq && er < need_eq) {
-          const uint32_t pos = n_gt + er;
-          if (pos < (uint32_t)KP) mysbuf[pos] = entry(u, (uint32_t)c);
+      gt_run += (uint32_t)__builtin_popcountll(gb);
+      const bool eq = valid && u == Vh;
+      const uint64_t eb = __builtin_amdgcn_uicmp(u, Vh, 32) & vb;       // u == Vh
+      if (eb != 0) {  // ties with the k-th key are rare: skip the step otherwise
+        if (eq) {
+          const uint32_t er = __builtin_amdgcn_mbcnt_hi((uint32_t)(eb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)eb, eq_run));
+          const uint32_t pos = ngt + er;
+          if (er < need && pos < (uint32_t)KP) sb[pos] = entry(u, (uint32_t)c);
         }
-        eq_run += half ? (uint32_t)__builtin_popcount(ehi) : e_lo_cnt;
+        eq_run += (uint32_t)__builtin_popcountll(eb);
       }
     }
-  }
-  const uint32_t eq_taken = eq_run < need_eq ? eq_run : need_eq;
-  if (V == kNegInfKey) {
-    // the remaining ties are masked candidates nv, nv+1, ...
-    for (uint32_t j = (uint32_t)hl; j < need_eq - eq_taken; j += 32) {
-      const uint32_t pos = n_gt + eq_taken + j;
-      if (pos < (uint32_t)KP) mysbuf[pos] = entry(kNegInfKey, (uint32_t)nv + j);
+    const uint32_t eq_taken = eq_run < need ? eq_run : need;
+    if (Vh == kNegInfKey) {
+      // the remaining ties are masked candidates nv, nv+1, ...
+      for (uint32_t j = (uint32_t)lane; j < need - eq_taken; j += 64) {
+        const uint32_t pos = ngt + eq_taken + j;
+        if (pos < (uint32_t)KP) sb[pos] = entry(kNegInfKey, (uint32_t)nvh + j);
+      }
     }
   }
   const uint32_t nsel = real ? K : 0u;
