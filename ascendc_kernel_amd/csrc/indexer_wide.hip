@@ -99,11 +99,6 @@ __device__ __forceinline__ int n_valid_w(const WideParams& p, int t) {
   return n < p.T ? n : p.T;
 }
 
-__device__ __forceinline__ uint32_t order_key16(uint32_t sc) {
-  uint32_t u = (sc ^ ((sc & 0x8000u) ? 0xffffu : 0x8000u)) & 0xffffu;
-  if ((sc & 0x7fffu) > 0x7f80u) u = 0xffffu;  // NaN ranks above everything
-  return u;
-}
 
 // Full wave over a 256-bin histogram (bins ascending in key) kept as NC copies
 // kCopyStride words apart and summed here: the bin b with count(bins > b) < need <=
@@ -500,12 +495,17 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
   auto finalize = [&](int n) {
     if (y == 0 && hf == 1) {
       const float x1 = xbuf[((n & 1) * kTok + tl) * kTileC + col];
-      const float tot = KY == 1 ? (x1 + t0val) + t0val2 : t0val + x1;
-      uint32_t sc = f2bf(tot);
-      if (p.causal) sc = f2bf(bf2f(sc) + 0.0f);  // the reference adds the 0 / -inf mask
+      const float t4 = KY == 1 ? (x1 + t0val) + t0val2 : t0val + x1;
+      // The reference adds the 0 / -inf mask in bf16: bf16(bf16(x) + 0) = bf16(x + 0),
+      // which only turns -0 into +0.
+      const float tot = p.causal ? t4 + 0.0f : t4;
+      const uint32_t sc = f2bf(tot);
       const int c = kTileC * (nbase + n) + col;
       if (c < nv) {
-        const uint16_t v = (uint16_t)(p.graw ? sc : order_key16(sc));
+        // order key: the bf16's sign is tot's (NaN aside), one arithmetic shift
+        const uint32_t neg = (uint32_t)((int32_t)__builtin_bit_cast(uint32_t, tot) >> 31);
+        const uint16_t key = __builtin_isnan(tot) ? (uint16_t)0xffffu : (uint16_t)(sc ^ (neg | 0x8000u));
+        const uint16_t v = (uint16_t)(p.graw ? sc : key);
         if constexpr (kFused) mykeys[c] = v;
         else if (gdst != nullptr) gdst[c] = v;
       }
