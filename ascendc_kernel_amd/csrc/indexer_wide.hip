@@ -140,6 +140,44 @@ __device__ __forceinline__ int find_bin64(const uint32_t* hist, int lane, uint32
   return __shfl(fb, src, 64);
 }
 
+// The occupied bins (non-zero total over NC copies) at or above lo_bin of a 256-bin
+// histogram, ranked from the top, by one wave: byte b of map (64 words of LDS) becomes
+// 255 - #(occupied bins above b) for every such bin b (other bytes: 0). Returns the
+// number of those bins.
+template <int NC>
+__device__ __forceinline__ int rank_map64(const uint32_t* hist, int lane, int lo_bin, uint32_t* map) {
+  u32x4 v = *reinterpret_cast<const u32x4*>(hist + 4 * lane);
+#pragma unroll
+  for (int c = 1; c < NC; ++c) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(hist + c * kCopyStride + 4 * lane);
+    v[0] += w[0];
+    v[1] += w[1];
+    v[2] += w[2];
+    v[3] += w[3];
+  }
+  uint32_t occ = 0u;  // bit i: bin 4 lane + i
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (v[i] != 0u && 4 * lane + i >= lo_bin) occ |= 1u << i;
+  const uint32_t local = (uint32_t)__builtin_popcount(occ);
+  uint32_t incl = local;  // occupied bins in lanes >= lane
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl(incl, (lane + off) & 63, 64);
+    if (lane + off < 64) incl += o;
+  }
+  uint32_t above = incl - local;
+  uint32_t word = 0u;
+#pragma unroll
+  for (int i = 3; i >= 0; --i)
+    if ((occ >> i) & 1u) {
+      word |= (255u - above) << (8 * i);
+      ++above;
+    }
+  map[lane] = word;
+  return __shfl((int)incl, 0, 64);
+}
+
 // hist[bin] += 1 for the active lanes of a wave, one LDS atomic per distinct bin
 // (the high bytes of a row's order keys fall into a handful of bins).
 __device__ __forceinline__ void hist_add_grouped(uint32_t* hist, uint32_t bin, bool active, int lane) {
@@ -173,11 +211,17 @@ __device__ __forceinline__ uint32_t keep_equal(uint32_t m, uint32_t b, uint32_t 
 // m &= ~(ballot ^ sext(bit)), one v_bitop3 per half), which gives each value its
 // rank among equal digits of the chunk so far (a per-wave running count per digit
 // in wr). The digit totals of all waves then give every (wave, digit) its output
-// start. Inlined so that src, dst and wr are addressed as LDS.
+// start. Inlined so that src, dst and wr are addressed as LDS. src and dst may be the
+// same buffer (every value is read into registers before the first barrier).
+// NB < 8: every value's digit has its bits NB..7 equal, so NB ballots tell the
+// digits apart. kRemap: each value's byte 3 is replaced, as it is read, by
+// remap[byte 3] (bytes of LDS); the values then carry it to dst.
 // wr: NW * 256 words, wt: NW words of LDS.
-template <int NW>
+template <int NW, int NB = 8, bool kRemap = false>
 __device__ __forceinline__ void radix_pass_desc(const uint32_t* src, uint32_t* dst, int n, int sh,
-                                                uint32_t* wr, uint32_t* wt, int tt) {
+                                                uint32_t* wr, uint32_t* wt, int tt,
+                                                const uint8_t* remap = nullptr) {
+  static_assert(NB >= 1 && NB <= 8, "digit bits");
   constexpr int kR = kMaxK / (64 * NW);  // rounds per wave at most
   const int lane = tt & 63, wv = tt >> 6;
   const int chunk = ((n + NW - 1) / NW + 63) & ~63;
@@ -191,22 +235,23 @@ __device__ __forceinline__ void radix_pass_desc(const uint32_t* src, uint32_t* d
   for (int r = 0; r < kR; ++r) {
     const int c = c_beg + 64 * r + lane;
     const bool act = c < c_end;
-    const uint32_t v = act ? src[c] : 0u;
+    uint32_t v = act ? src[c] : 0u;
+    if constexpr (kRemap) v = (v & 0x00ffffffu) | ((uint32_t)remap[v >> 24] << 24);
     const uint32_t d = 255u - ((v >> sh) & 255u);
     const uint64_t am = __ballot(act);
     uint32_t mlo = (uint32_t)am, mhi = (uint32_t)(am >> 32);
-    // equal digits <=> equal bits sh .. sh+7 of v; the eight ballots are all taken
+    // equal digits <=> equal bits sh .. sh+NB-1 of v; the ballots are all taken
     // before they are used
-    uint32_t sx[8];
-    uint64_t bb[8];
+    uint32_t sx[NB];
+    uint64_t bb[NB];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < NB; ++b) {
       sx[b] = (uint32_t)__builtin_amdgcn_sbfe((int)v, sh + b, 1);  // 0 or ~0
       asm("" : "+v"(sx[b]));  // the ballot tests sx itself (one compare)
       bb[b] = __ballot(sx[b] != 0u);
     }
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < NB; ++b) {
       mlo = keep_equal(mlo, (uint32_t)bb[b], sx[b]);
       mhi = keep_equal(mhi, (uint32_t)(bb[b] >> 32), sx[b]);
     }
@@ -623,7 +668,10 @@ __global__ __launch_bounds__(512) void ix_wide_kernel(WideParams p) {
 //   2. one workgroup scan of the per-thread counts (#(> kth) | #(== kth) << 16)
 //      places every pick: [> kth] at [0, n_gt) and the first K - n_gt [== kth]
 //      after them, each in index order;
-//   3. stable two-pass radix sort of the picks on the key (descending), int64 out.
+//   3. stable two-pass LSD radix sort of the picks on the key (descending), in place:
+//      the low byte, then the high byte's rank among the bins that hold picks (from
+//      the high-byte histogram, which every row takes), in as many ballots per round
+//      as that number of bins needs; int64 out.
 struct SelParams {
   const uint16_t* keys;  // [B*S, kstride], kstride = T rounded up to a multiple of 4
   int64_t kstride;
@@ -651,9 +699,9 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   extern __shared__ __align__(16) uint8_t smem[];
   uint32_t* hist = reinterpret_cast<uint32_t*>(smem);     // h1 | h2, then the radix counts
   uint32_t* wt = hist + sel_hist_words<NT>();              // [NW] wave totals
-  int32_t* sel = reinterpret_cast<int32_t*>(wt + NW);     // [4]
-  uint32_t* sortbuf = reinterpret_cast<uint32_t*>(sel + 4);  // [psort]
-  uint32_t* tmpbuf = sortbuf + p.psort;                    // [psort]
+  int32_t* sel = reinterpret_cast<int32_t*>(wt + NW);     // [8]
+  uint32_t* hmap = reinterpret_cast<uint32_t*>(sel + 8);  // [64]: 256 bytes, the high bytes' ranks
+  uint32_t* sortbuf = hmap + 64;                           // [psort]
   const int tt = threadIdx.x;
   const int lane = tt & 63, wv = tt >> 6;
   const int64_t row = blockIdx.x;
@@ -691,21 +739,28 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   for (int i = tt; i < kH2 + 256; i += NT) hist[i] = (i == 0) ? 0u - pad : 0u;
   __syncthreads();
   uint32_t kth = 0u, n_gt = (uint32_t)nv, need_eq = 0u;
-  if (selecting) {
+  {
     uint32_t* h1 = hist + (lane & (kH1Copies - 1)) * kCopyStride;
 #pragma unroll
     for (int e = 0; e < KPT; ++e)
       if ((e >> 2) < npiece) atomicAdd(&h1[key_of(e) >> 8], 1u);
-    __syncthreads();
-    if (wv == 0) {
-      uint32_t gt;
-      const int b1 = find_bin64<kH1Copies>(hist, lane, (uint32_t)K, gt);
-      if (lane == 0) {
-        sel[0] = b1;
-        sel[1] = (int32_t)gt;
-      }
+  }
+  __syncthreads();
+  // Wave 0: the high-byte bin of the K-th key (when selecting), and the ranks of the
+  // bins that hold picks: every occupied bin at or above that one (above bin 0
+  // without selection).
+  if (wv == 0) {
+    uint32_t gt = 0u;
+    const int b1 = selecting ? find_bin64<kH1Copies>(hist, lane, (uint32_t)K, gt) : 0;
+    const int nocc = rank_map64<kH1Copies>(hist, lane, b1, hmap);
+    if (lane == 0) {
+      sel[0] = b1;
+      sel[1] = (int32_t)gt;
+      sel[4] = nocc;
     }
-    __syncthreads();
+  }
+  __syncthreads();
+  if (selecting) {
     const uint32_t b1 = (uint32_t)sel[0];
     if (b1 == 0u && tt == 0) atomicSub(&hist[kH2], pad);
 #pragma unroll
@@ -770,9 +825,25 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
     oe += q ? 1u : 0u;
   }
   const int count = selecting ? K : nv;
+  const int nocc = __builtin_amdgcn_readfirstlane(sel[4]);
   __syncthreads();
-  radix_pass_desc<NW>(sortbuf, tmpbuf, count, 16, hist, wt, tt);
-  radix_pass_desc<NW>(tmpbuf, sortbuf, count, 24, hist, wt, tt);
+  // Stable LSD radix sort of the picks on the key, descending, in place: the low byte,
+  // then the high byte's rank among the nocc bins that hold picks (the first pass
+  // writes it over the high byte as 255 - rank), which takes ceil(log2 nocc) ballots
+  // per round instead of 8 (one bin: no second pass).
+  radix_pass_desc<NW, 8, true>(sortbuf, sortbuf, count, 16, hist, wt, tt,
+                               reinterpret_cast<const uint8_t*>(hmap));
+  switch (nocc <= 1 ? 0 : 32 - __builtin_clz((uint32_t)(nocc - 1))) {
+    case 0: break;
+    case 1: radix_pass_desc<NW, 1>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
+    case 2: radix_pass_desc<NW, 2>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
+    case 3: radix_pass_desc<NW, 3>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
+    case 4: radix_pass_desc<NW, 4>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
+    case 5: radix_pass_desc<NW, 5>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
+    case 6: radix_pass_desc<NW, 6>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
+    case 7: radix_pass_desc<NW, 7>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
+    default: radix_pass_desc<NW, 8>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
+  }
   int64_t* out_row = p.out + row * K;
   for (int j = tt; j < K; j += NT) {
     const uint32_t comp = sortbuf[j];
@@ -913,7 +984,7 @@ int dsa_indexer_wide_launch(const void* q, const void* kv_cache, int64_t kv_batc
     void (*sfn)(SelParams) = wide_rows ? ix_select_kernel<1024> : ix_select_kernel<256>;
     const int snt = wide_rows ? 1024 : 256;
     const size_t smem2 = (size_t)(wide_rows ? sel_hist_words<1024>() : sel_hist_words<256>()) * 4 +
-                         (size_t)(snt / 64) * 4 + 16 + (size_t)ps * 8;
+                         (size_t)(snt / 64) * 4 + 32 + 256 + (size_t)ps * 4;
     if (dsa_host::ensure_dyn_lds((const void*)sfn, (int)smem2) != DSA_OK) return DSA_ERR_LAUNCH;
     hipLaunchKernelGGL(sfn, dim3((unsigned)(b * s)), dim3(snt), smem2, stream, sp);
     if (hipGetLastError() != hipSuccess) return DSA_ERR_LAUNCH;
