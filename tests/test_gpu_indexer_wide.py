@@ -175,6 +175,37 @@ def test_wide_shapes_and_modes(gpu, case):
     _check_equal(m(x, qr, start_pos, offset), r(x, qr, start_pos, offset), f"wide{case}")
 
 
+@pytest.mark.parametrize("seqlen", [256, 4])
+@pytest.mark.parametrize("keys", ["spread24", "spread60", "equal"])
+def test_wide_select_key_spreads(gpu, seqlen, keys):
+    """Top-2048 of 4096 candidates (start_pos 4096 - seqlen, no mask) with the key rows
+    scaled by 2^e per candidate, so that the picks' scores span many binades of both
+    signs (the selector's second radix pass then tells 15-96 high-byte bins apart), or
+    with every key row equal (one score per token: one bin, the second pass skipped,
+    the order decided by the index alone). 256 tokens take the 256-thread selector,
+    4 tokens the 1024-thread one."""
+    end, topk = 4096, 2048
+    start_pos = end - seqlen
+    args = _args(end, topk)
+    m, r = _pair(args, 77, end, 1, gpu, wstd=0.02)
+    g = torch.Generator().manual_seed(78)
+    with torch.no_grad():
+        if keys == "equal":
+            m.kv_cache.copy_(m.kv_cache[:, :1].clone().expand_as(m.kv_cache))
+        else:
+            span = int(keys[len("spread"):])
+            e = torch.randint(-span, span + 1, (end,), generator=g).float()
+            m.kv_cache.mul_(torch.exp2(e).to(gpu)[None, :, None].to(torch.bfloat16))
+    assert m.kv_cache is r.kv_cache
+    x = torch.randn(1, seqlen, 7168, generator=g).to(torch.bfloat16).to(gpu)
+    qr = torch.randn(1, seqlen, 1536, generator=g).to(torch.bfloat16).to(gpu)
+    _say("select key spread", seqlen, keys)
+    with torch.no_grad():
+        got = m(x, qr, start_pos, 3)
+        want = r(x, qr, start_pos, 3)
+    _check_equal(got, want, f"spread-{keys}-{seqlen}")
+
+
 @pytest.mark.parametrize("input_seed", [43, None])
 def test_full_shape_c5_indexer(gpu, input_seed):
     """configs[4] indexer: x[1,8192,7168], qr[1,8192,1536], kv_cache[1,8192,128], W ~ N(0, 0.02),
