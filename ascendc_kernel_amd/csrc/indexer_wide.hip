@@ -696,6 +696,11 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   constexpr int NW = NT / 64;
   constexpr int KPT = kMaxT / NT;  // keys per thread
   constexpr int KW = KPT / 4;      // 8-byte words per thread
+  // The second sort pass on the high byte's rank (below) saves VALU work where rows
+  // share the CU (256 threads); for one row per workgroup of 1024 threads (decode),
+  // whose latency is the step's, the rank map's extra serial steps cost more than
+  // the ballots they save, so that instantiation sorts on both bytes in full.
+  constexpr bool kNarrow = NT <= 256;
   extern __shared__ __align__(16) uint8_t smem[];
   uint32_t* hist = reinterpret_cast<uint32_t*>(smem);     // h1 | h2, then the radix counts
   uint32_t* wt = hist + sel_hist_words<NT>();              // [NW] wave totals
@@ -739,7 +744,7 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   for (int i = tt; i < kH2 + 256; i += NT) hist[i] = (i == 0) ? 0u - pad : 0u;
   __syncthreads();
   uint32_t kth = 0u, n_gt = (uint32_t)nv, need_eq = 0u;
-  {
+  if (kNarrow || selecting) {
     uint32_t* h1 = hist + (lane & (kH1Copies - 1)) * kCopyStride;
 #pragma unroll
     for (int e = 0; e < KPT; ++e)
@@ -752,7 +757,7 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   if (wv == 0) {
     uint32_t gt = 0u;
     const int b1 = selecting ? find_bin64<kH1Copies>(hist, lane, (uint32_t)K, gt) : 0;
-    const int nocc = rank_map64<kH1Copies>(hist, lane, b1, hmap);
+    const int nocc = kNarrow ? rank_map64<kH1Copies>(hist, lane, b1, hmap) : 256;
     if (lane == 0) {
       sel[0] = b1;
       sel[1] = (int32_t)gt;
@@ -831,9 +836,9 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   // then the high byte's rank among the nocc bins that hold picks (the first pass
   // writes it over the high byte as 255 - rank), which takes ceil(log2 nocc) ballots
   // per round instead of 8 (one bin: no second pass).
-  radix_pass_desc<NW, 8, true>(sortbuf, sortbuf, count, 16, hist, wt, tt,
-                               reinterpret_cast<const uint8_t*>(hmap));
-  switch (nocc <= 1 ? 0 : 32 - __builtin_clz((uint32_t)(nocc - 1))) {
+  radix_pass_desc<NW, 8, kNarrow>(sortbuf, sortbuf, count, 16, hist, wt, tt,
+                                  reinterpret_cast<const uint8_t*>(hmap));
+  switch (!kNarrow ? 8 : nocc <= 1 ? 0 : 32 - __builtin_clz((uint32_t)(nocc - 1))) {
     case 0: break;
     case 1: radix_pass_desc<NW, 1>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
     case 2: radix_pass_desc<NW, 2>(sortbuf, sortbuf, count, 24, hist, wt, tt); break;
