@@ -744,7 +744,9 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   for (int i = tt; i < kH2 + 256; i += NT) hist[i] = (i == 0) ? 0u - pad : 0u;
   __syncthreads();
   uint32_t kth = 0u, n_gt = (uint32_t)nv, need_eq = 0u;
-  if (kNarrow || selecting) {
+  // A wave whose keys all lie past nv (causal rows) skips the per-key loops.
+  const bool wlive = __builtin_amdgcn_readfirstlane(wv) * (64 * KPT) < nv;
+  if ((kNarrow || selecting) && wlive) {
     uint32_t* h1 = hist + (lane & (kH1Copies - 1)) * kCopyStride;
 #pragma unroll
     for (int e = 0; e < KPT; ++e)
@@ -768,10 +770,12 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   if (selecting) {
     const uint32_t b1 = (uint32_t)sel[0];
     if (b1 == 0u && tt == 0) atomicSub(&hist[kH2], pad);
+    if (wlive) {
 #pragma unroll
-    for (int e = 0; e < KPT; ++e) {
-      const uint32_t u = key_of(e);
-      if ((e >> 2) < npiece && (u >> 8) == b1) atomicAdd(&hist[kH2 + (u & 255u)], 1u);
+      for (int e = 0; e < KPT; ++e) {
+        const uint32_t u = key_of(e);
+        if ((e >> 2) < npiece && (u >> 8) == b1) atomicAdd(&hist[kH2 + (u & 255u)], 1u);
+      }
     }
     __syncthreads();
     if (wv == 0) {
@@ -793,17 +797,19 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   // Without selection every key > 0 is a pick; kth >= 0x007f when selecting, so
   // the 0 marks never count.
   const uint32_t kth_e = selecting ? kth : 0xffffffffu;
-  uint32_t cnt = 0u;
+  uint32_t cnt = 0u, incl = 0u;
+  if (wlive) {
 #pragma unroll
-  for (int e = 0; e < KPT; ++e) {
-    const uint32_t u = key_of(e);
-    cnt += (u > kth ? 1u : 0u) + (u == kth_e ? 0x10000u : 0u);
-  }
-  uint32_t incl = cnt;
+    for (int e = 0; e < KPT; ++e) {
+      const uint32_t u = key_of(e);
+      cnt += (u > kth ? 1u : 0u) + (u == kth_e ? 0x10000u : 0u);
+    }
+    incl = cnt;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
-    if (lane >= off) incl += o;
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
+      if (lane >= off) incl += o;
+    }
   }
   if (lane == 63) wt[wv] = incl;
   __syncthreads();
@@ -814,20 +820,22 @@ __global__ __launch_bounds__(NT) void ix_select_kernel(SelParams p) {
   const uint32_t ibase = 0xffffu - (uint32_t)c0;
   // The comparisons are recomputed below rather than kept from the count loop (64
   // lane masks of it would not fit in the scalar registers).
+  if (wlive) {
 #pragma unroll
-  for (int i = 0; i < KW; ++i) asm volatile("" : "+v"(kw[i]));
+    for (int i = 0; i < KW; ++i) asm volatile("" : "+v"(kw[i]));
 #pragma unroll
-  for (int e = 0; e < KPT; ++e) {
-    const uint32_t u = key_of(e);
-    const bool g = u > kth, q = u == kth_e;
-    const bool ok = g | (q & (oe < oe_end));
-    const uint32_t pos = g ? og : oe;
-    // (u << 16) | (index bits): one v_perm of the key's 16-bit half and ibase - e
-    const uint32_t w = (e & 2) ? kw[e >> 2].y : kw[e >> 2].x;
-    const uint32_t comp = __builtin_amdgcn_perm(w, ibase - (uint32_t)e, (e & 1) ? 0x07060100u : 0x05040100u);
-    if (ok) sortbuf[pos] = comp;
-    og += g ? 1u : 0u;
-    oe += q ? 1u : 0u;
+    for (int e = 0; e < KPT; ++e) {
+      const uint32_t u = key_of(e);
+      const bool g = u > kth, q = u == kth_e;
+      const bool ok = g | (q & (oe < oe_end));
+      const uint32_t pos = g ? og : oe;
+      // (u << 16) | (index bits): one v_perm of the key's 16-bit half and ibase - e
+      const uint32_t w = (e & 2) ? kw[e >> 2].y : kw[e >> 2].x;
+      const uint32_t comp = __builtin_amdgcn_perm(w, ibase - (uint32_t)e, (e & 1) ? 0x07060100u : 0x05040100u);
+      if (ok) sortbuf[pos] = comp;
+      og += g ? 1u : 0u;
+      oe += q ? 1u : 0u;
+    }
   }
   const int count = selecting ? K : nv;
   const int nocc = __builtin_amdgcn_readfirstlane(sel[4]);
