@@ -315,7 +315,8 @@ int dsa_indexer_pack_projection_weights(const void* wq, int64_t n, int64_t k, co
  * accumulate in fp32 over k in ascending order and round once to bf16; RoPE as in
  * dsa_indexer_q_proj. That equals torch-ROCm's F.linear where hipBLASLt runs a kernel
  * without split-k: for wq (k = 256) from 17 tokens up, for weights_proj (k = 1024, 16
- * outputs) only from about 20,000 tokens (below, hipBLASLt sums k over 4 wave groups);
+ * outputs) only from about 15,400 tokens (below, hipBLASLt sums k over 4 wave groups, which
+ * changes ~1.7e-4 of the outputs);
  * the drop-in Model calls this entry point only inside the token range its GPU sweep covers.
  *
  *   qr            bf16 [m, k]      m = b * s_len token rows, k == 256

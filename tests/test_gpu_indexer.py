@@ -185,6 +185,36 @@ SMALL = [
 ]
 
 
+@pytest.mark.parametrize("keys", ["spread30", "equal", "equal_but_8"])
+@pytest.mark.parametrize("start_pos,seqlen", [(2536, 64), (0, 600)])
+def test_select_key_spreads(gpu, keys, start_pos, seqlen):
+    """The 16-head kernel's selection with key rows scaled by 2^e per candidate (scores
+    over many binades of both signs), with every key row equal (all valid candidates tie:
+    the picks are decided by the index alone) and with all rows equal but 8 (ties at the
+    k-th key). Without the mask (start_pos > 0, 650 candidates) and causal (start_pos 0,
+    masked candidates filled with -1)."""
+    batch, topk, kv_rows = 2, 128, 650
+    args = oix.IndexerArgs(max_batch_size=batch, max_seq_len=2600, dim=1024, q_lora_rank=256,
+                           rope_head_dim=32, index_n_heads=16, index_head_dim=64, index_topk=topk)
+    m, r = _pair(args, 300 + seqlen, batch, kv_rows, gpu)
+    g = torch.Generator().manual_seed(301)
+    with torch.no_grad():
+        if keys == "spread30":
+            e = torch.randint(-30, 31, (kv_rows,), generator=g).float()
+            m.kv_cache.mul_(torch.exp2(e).to(gpu)[None, :, None].to(torch.bfloat16))
+        else:
+            keep = m.kv_cache[:, :8].clone()
+            m.kv_cache.copy_(m.kv_cache[:, 8:9].clone().expand_as(m.kv_cache))
+            if keys == "equal_but_8":
+                sel = torch.randperm(kv_rows, generator=g)[:8].to(gpu)
+                m.kv_cache[:, sel] = keep
+    assert m.kv_cache is r.kv_cache
+    x = torch.randn(batch, seqlen, 1024, generator=g).to(torch.bfloat16).to(gpu)
+    qr = torch.randn(batch, seqlen, 256, generator=g).to(torch.bfloat16).to(gpu)
+    _say("select key spread", keys, start_pos, seqlen)
+    _check_equal(m(x, qr, start_pos, 2), r(x, qr, start_pos, 2), f"spread-{keys}-{start_pos}")
+
+
 @pytest.mark.parametrize("case", SMALL)
 def test_shapes_and_modes(gpu, case):
     batch, seqlen, start_pos, offset, topk, kv_rows = case

@@ -116,7 +116,7 @@ def test_projection_route_boundaries():
             assert r(m) == want, m
     assert r(32768) == "both" and r(32769) == "torch"   # hipBLASLt splits wq_b's k sum above 32,768
     assert r(16384) == "q" and r(16385) == "both"
-    assert r(63) == "torch" and r(64) == r(140) == "both" and r(141) == "q"   # weights_proj: 17 .. 140
+    assert r(63) == "torch" and r(64) == r(140) == r(15360) == "q" and r(15361) == "both"   # weights_proj
     assert r(8 * 2600, build_ok=False) == "torch"      # another torch / hipBLASLt build or CU count
     assert r(8 * 2600, on_gpu=False) == r(8 * 2600, bf16=False) == "torch"
     assert r(8 * 2600, dim=2048) == r(8 * 2600, n_w=32) == "q"
