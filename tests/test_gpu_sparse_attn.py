@@ -107,6 +107,22 @@ def test_shapes_and_masks(gpu, case):
     _compare(out, ref, f"case{case}")
 
 
+@pytest.mark.parametrize("variant,n_kv,topk", [(_native.DSA_SA_MULTIPLICITY, 32, 16),
+                                                (_native.DSA_SA_GATHER, 32, 16),
+                                                (_native.DSA_SA_GATHER, 3000, 512)])
+@pytest.mark.parametrize("qs,ks", [(16.0, 8.0), (0.0625, 1.0)])
+def test_large_and_flat_score_ranges(gpu, variant, n_kv, topk, qs, ks):
+    """q and kv scaled by powers of two (exact in bf16): scores with a spread of ~±150 (a
+    softmax that is nearly one-hot, the running max raised many times across blocks) and
+    nearly flat ones (every weight close to the others)."""
+    q, kv, idx, sink = _case(2, 40, 64, n_kv, topk, 21, 0.1, 1.0)
+    q, kv = (q.float() * qs).to(torch.bfloat16), (kv.float() * ks).to(torch.bfloat16)
+    _say("case score range", variant, n_kv, topk, qs, ks)
+    out = _native.sparse_attn_fwd(q, kv, idx, sink, 128 ** -0.5, variant=variant)
+    ref = osa.sparse_attn_ref(q, kv, sink, idx, 128 ** -0.5)
+    _compare(out, ref, f"range-{variant}-{n_kv}-{qs}-{ks}", atol=1e-2 * ks, rtol=1e-2)
+
+
 def test_fully_masked_tokens_and_single_index(gpu):
     q, kv, idx, sink = _case(1, 6, 64, 32, 16, 11, 0.0, 1.5)
     idx[0, 1] = -1

@@ -82,6 +82,18 @@ def test_mla_shapes_and_masks(gpu, case):
     _compare(out, ref, f"mla{case}")
 
 
+@pytest.mark.parametrize("qs,ks", [(16.0, 4.0), (0.0625, 1.0)])
+def test_mla_large_and_flat_score_ranges(gpu, qs, ks):
+    """q and the latent rows scaled by powers of two (exact in bf16): nearly one-hot
+    softmax rows with the running max raised across blocks, and nearly flat ones."""
+    q, kv, idx, sink = _case(1, 12, 128, 3000, 1024, 22, 0.1, 1.0)
+    q, kv = (q.float() * qs).to(torch.bfloat16), (kv.float() * ks).to(torch.bfloat16)
+    _say("mla score range", qs, ks)
+    out = _native.sparse_mla_fwd(q, kv, idx, sink, SCALE, DV)
+    ref = osa.sparse_attn_ref(q, kv, sink, idx, SCALE, v_dim=DV)
+    _compare(out, ref, f"mla-range-{qs}-{ks}", atol=1e-2 * ks, rtol=1e-2)
+
+
 def test_mla_masked_tokens_oob_and_wide_rows(gpu):
     """Fully masked tokens give 0; indices >= n_kv count as masked; kv rows wider than 576."""
     q, kv, idx, sink = _case(1, 6, 64, 50, 40, 6, 0.0, 1.0, kv_dim=640)
