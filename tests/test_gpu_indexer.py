@@ -215,6 +215,30 @@ def test_select_key_spreads(gpu, keys, start_pos, seqlen):
     _check_equal(m(x, qr, start_pos, 2), r(x, qr, start_pos, 2), f"spread-{keys}-{start_pos}")
 
 
+def test_noncontiguous_inputs(gpu):
+    """x and qr as transposed views and a kv_cache with a padded row stride (the reference
+    accepts any strides): the drop-in Model takes the unplanned path and gives the same
+    indices as the reference and as its contiguous inputs."""
+    batch, seqlen, topk = 2, 300, 64
+    args = oix.IndexerArgs(max_batch_size=batch, max_seq_len=2600, dim=1024, q_lora_rank=256,
+                           rope_head_dim=32, index_n_heads=16, index_head_dim=64, index_topk=topk)
+    m, r = _pair(args, 401, batch, 650, gpu)
+    g = torch.Generator().manual_seed(402)
+    x = torch.randn(batch, 1024, seqlen, generator=g).to(torch.bfloat16).to(gpu).transpose(1, 2)
+    qr = torch.randn(batch, 256, seqlen, generator=g).to(torch.bfloat16).to(gpu).transpose(1, 2)
+    assert not x.is_contiguous() and not qr.is_contiguous()
+    _say("case non-contiguous x, qr")
+    want = r(x, qr, 0, 1)
+    _check_equal(m(x, qr, 0, 1), want, "noncontig")
+    _check_equal(m(x.contiguous(), qr.contiguous(), 0, 1), want, "noncontig-copy")
+    # kv_cache rows with a stride of 96 elements (64 used)
+    kvp = torch.zeros(batch, 650, 96, dtype=torch.bfloat16, device=gpu)
+    kvp[..., :64] = m.kv_cache
+    m.kv_cache = kvp[..., :64]
+    r.kv_cache = kvp[..., :64]
+    _check_equal(m(x, qr, 0, 1), r(x, qr, 0, 1), "noncontig-kv")
+
+
 @pytest.mark.parametrize("case", SMALL)
 def test_shapes_and_modes(gpu, case):
     batch, seqlen, start_pos, offset, topk, kv_rows = case

@@ -123,6 +123,25 @@ def test_large_and_flat_score_ranges(gpu, variant, n_kv, topk, qs, ks):
     _compare(out, ref, f"range-{variant}-{n_kv}-{qs}-{ks}", atol=1e-2 * ks, rtol=1e-2)
 
 
+@pytest.mark.parametrize("n_kv,topk", [(32, 16), (500, 96)])
+def test_noncontiguous_inputs(gpu, n_kv, topk):
+    """q, kv and topk_idxs as strided views (the reference accepts any strides): the module
+    gives the output of their contiguous copies."""
+    q, kv, idx, sink = _case(2, 30, 64, n_kv, topk, 23, 0.1, 0.5)
+    qn = q.transpose(1, 2).contiguous().transpose(1, 2)            # [b, m, h, d] strided
+    kvn = torch.cat([kv, kv], dim=-1)[..., :128]                   # row stride 256
+    idxn = idx.transpose(1, 2).contiguous().transpose(1, 2)        # [b, m, topk] strided
+    assert not (qn.is_contiguous() or kvn.is_contiguous() or idxn.is_contiguous())
+    model = t1.Model(64, 128).to(gpu)
+    with torch.no_grad():
+        model.attn_sink.copy_(sink)
+    _say("case non-contiguous", n_kv, topk)
+    got = model(qn, kvn, idxn)
+    want = model(q, kv, idx)
+    assert torch.equal(got, want)
+    _compare(got, osa.sparse_attn_ref(q, kv, sink, idx, 128 ** -0.5), f"noncontig-{n_kv}")
+
+
 def test_fully_masked_tokens_and_single_index(gpu):
     q, kv, idx, sink = _case(1, 6, 64, 32, 16, 11, 0.0, 1.5)
     idx[0, 1] = -1
