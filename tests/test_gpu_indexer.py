@@ -182,6 +182,9 @@ SMALL = [
     (5, 3333, 0, 0, 64, 834),
     (4, 5000, 2000, 4, 128, 1750),
     (8, 8187, 0, 0, 32, 2047),
+    # offsets beyond int32 (the output is int64: index + offset, -1 where masked)
+    (2, 300, 0, (1 << 33) + 5, 64, 650),
+    (1, 20, 500, -(1 << 40), 32, 650),
 ]
 
 

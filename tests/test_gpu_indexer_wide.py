@@ -159,6 +159,8 @@ WIDE = [
     (1, 3004, 0, 1024, 2),
     (2, 1, 0, 3, 1),      # T = 3
     (1, 0, 0, 1, 1),      # T = 1: a single candidate (top-1 whatever its score)
+    (300, 0, (1 << 35) + 1, 256, 1),   # an offset beyond int32 (int64 output)
+    (2, 4000, -(1 << 36), 512, 1),
 ]
 
 
