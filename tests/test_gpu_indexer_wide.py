@@ -178,13 +178,14 @@ def test_wide_shapes_and_modes(gpu, case):
 
 
 @pytest.mark.parametrize("seqlen", [256, 4])
-@pytest.mark.parametrize("keys", ["spread24", "spread60", "equal"])
+@pytest.mark.parametrize("keys", ["spread24", "spread60", "equal", "equal_but_100"])
 def test_wide_select_key_spreads(gpu, seqlen, keys):
     """Top-2048 of 4096 candidates (start_pos 4096 - seqlen, no mask) with the key rows
     scaled by 2^e per candidate, so that the picks' scores span many binades of both
     signs (the selector's second radix pass then tells 15-96 high-byte bins apart), or
     with every key row equal (one score per token: one bin, the second pass skipped,
-    the order decided by the index alone). 256 tokens take the 256-thread selector,
+    the order decided by the index alone), or all equal but 100 (about 2,000 of the
+    2,048 picks tie at the k-th key). 256 tokens take the 256-thread selector,
     4 tokens the 1024-thread one."""
     end, topk = 4096, 2048
     start_pos = end - seqlen
@@ -192,8 +193,12 @@ def test_wide_select_key_spreads(gpu, seqlen, keys):
     m, r = _pair(args, 77, end, 1, gpu, wstd=0.02)
     g = torch.Generator().manual_seed(78)
     with torch.no_grad():
-        if keys == "equal":
+        if keys.startswith("equal"):
+            keep = m.kv_cache.clone()
             m.kv_cache.copy_(m.kv_cache[:, :1].clone().expand_as(m.kv_cache))
+            if keys == "equal_but_100":  # ~2,000 picks tie at the k-th key: index order decides
+                sel = torch.randperm(end, generator=g)[:100].to(gpu)
+                m.kv_cache[:, sel] = keep[:, sel]
         else:
             span = int(keys[len("spread"):])
             e = torch.randint(-span, span + 1, (end,), generator=g).float()
