@@ -63,14 +63,14 @@ def _settled_us(fn, reps, min_seconds=0.3):
 # clock) against a bf16 [8192 x 8192] x [8192 x 8192] torch.matmul. A regression past
 # ratio x calibration fails. Measured (copy 125.6 - 126.8 us, matmul 794 - 815 us; three
 # runs on each box): c2 0.935 - 0.947 (two boxes), c3 kernel 0.0523 - 0.0527, c3
-# projections 0.0276 - 0.0287, c3 Model.forward 0.0793 - 0.0808, c4 0.492 - 0.511 (two
+# projections 0.0276 - 0.0287, c3 Model.forward 0.0793 - 0.0835 (four boxes), c4 0.492 - 0.511 (two
 # boxes), c5 MLA 6.50 - 6.87 (two boxes: the ratio that varies most between boxes), c5
 # indexer kernels 0.845 - 0.847 (two boxes, the current selector). Each budget sits 5 %
 # above the largest ratio measured on two boxes, 7 % above one measured on one box (the
 # spread between boxes is up to ~6 %); configs[1]: 0.99, a 125 us equivalent at the
 # copy's 126 us.
 RATIO_BUDGET = {"c2": ("copy", 0.99), "c3_kernel": ("matmul", 0.0564), "c3_proj": ("matmul", 0.0301),
-                "c3_model": ("matmul", 0.0865), "c4": ("matmul", 0.536), "c5_mla": ("matmul", 7.21),
+                "c3_model": ("matmul", 0.0877), "c4": ("matmul", 0.536), "c5_mla": ("matmul", 7.21),
                 "c5_indexer": ("matmul", 0.89)}
 
 
