@@ -69,12 +69,13 @@ class IndexerRef(nn.Module):
         self.compress_ratio = compress_ratio
         self.kv_cache = kv_cache
         self.freqs_cis = freqs_cis
+        self.einsum_rows = None  # see index_scores
 
     def forward(self, x, qr, start_pos: int, offset: int):
         return indexer_forward(self.wq_b.weight, self.weights_proj.weight, self.kv_cache,
                                self.freqs_cis, x, qr, start_pos, offset, self.n_heads,
                                self.head_dim, self.rope_head_dim, self.index_topk,
-                               self.compress_ratio)
+                               self.compress_ratio, self.einsum_rows)
 
 
 def apply_rotary_emb(x: torch.Tensor, freqs_cis: torch.Tensor) -> torch.Tensor:
@@ -87,15 +88,27 @@ def apply_rotary_emb(x: torch.Tensor, freqs_cis: torch.Tensor) -> torch.Tensor:
 
 
 def index_scores(wq, ww, kv_cache, freqs_cis, x, qr, start_pos, n_heads, head_dim, rope_head_dim,
-                 ratio) -> torch.Tensor:
-    """task2_v0_ref.py:124-137: the bf16 [b, s, T] score after the mask."""
+                 ratio, einsum_rows=None) -> torch.Tensor:
+    """task2_v0_ref.py:124-137: the bf16 [b, s, T] score after the mask.
+
+    einsum_rows: when set, the einsum of :133 runs on at most that many tokens of one
+    batch at a time. Every output is still one fp32 dot product over head_dim rounded
+    once to bf16; what changes is the GEMM algorithm torch-ROCm picks for the call, and
+    with it the fp32 summation order over head_dim, which differs between algorithms
+    for a few products in a billion (measured on the MI355X)."""
     bsz, seqlen, _ = x.size()
     fc = freqs_cis[start_pos:start_pos + seqlen]                               # :125
     end_pos = start_pos + seqlen                                               # :128
     q = F.linear(qr, wq).unflatten(-1, (n_heads, head_dim))                    # :129-130
     apply_rotary_emb(q[..., -rope_head_dim:], fc)                              # :131
     w = F.linear(x, ww) * (head_dim ** -0.5 * n_heads ** -0.5)                 # :132
-    score = torch.einsum("bshd,btd->bsht", q, kv_cache[:bsz, :end_pos // ratio])  # :133
+    kv = kv_cache[:bsz, :end_pos // ratio]
+    if einsum_rows is None:
+        score = torch.einsum("bshd,btd->bsht", q, kv)                          # :133
+    else:
+        score = torch.cat([torch.cat([torch.einsum("bshd,btd->bsht", q[i:i + 1, c:c + einsum_rows], kv[i:i + 1])
+                                      for c in range(0, seqlen, einsum_rows)], dim=1)
+                           for i in range(bsz)])
     score = (score.relu_() * w.unsqueeze(-1)).sum(dim=2)                       # :134
     if start_pos == 0:                                                         # :135-137
         dev = x.device
@@ -120,10 +133,10 @@ def select_topk(score: torch.Tensor, start_pos: int, offset: int, index_topk: in
 
 
 def indexer_forward(wq, ww, kv_cache, freqs_cis, x, qr, start_pos, offset, n_heads, head_dim,
-                    rope_head_dim, index_topk, ratio) -> torch.Tensor:
-    """task2_v0_ref.py:123-144."""
+                    rope_head_dim, index_topk, ratio, einsum_rows=None) -> torch.Tensor:
+    """task2_v0_ref.py:123-144 (einsum_rows: as in index_scores)."""
     score = index_scores(wq, ww, kv_cache, freqs_cis, x, qr, start_pos, n_heads, head_dim,
-                         rope_head_dim, ratio)
+                         rope_head_dim, ratio, einsum_rows)
     return select_topk(score, start_pos, offset, index_topk, ratio)
 
 

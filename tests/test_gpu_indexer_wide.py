@@ -70,8 +70,8 @@ def test_torch_head_sum_rule_64(gpu):
     assert not np.array_equal(other, want)  # the planted data tells the two orders apart
 
 
-def _args(seqlen, topk, rd=64):
-    return oix.IndexerArgs(max_batch_size=1, max_seq_len=seqlen, dim=7168, q_lora_rank=1536,
+def _args(seqlen, topk, rd=64, batch=1):
+    return oix.IndexerArgs(max_batch_size=batch, max_seq_len=seqlen, dim=7168, q_lora_rank=1536,
                            rope_head_dim=rd, index_n_heads=64, index_head_dim=128, index_topk=topk)
 
 
@@ -175,6 +175,49 @@ def test_wide_shapes_and_modes(gpu, case):
     qr = torch.randn(1, seqlen, 1536, generator=g).to(torch.bfloat16).to(gpu)
     _say("wide case", case)
     _check_equal(m(x, qr, start_pos, offset), r(x, qr, start_pos, offset), f"wide{case}")
+
+
+WIDE_BATCHES = [
+    # batch, kv_cache batch rows (max_batch_size), seqlen, start_pos, offset, topk, ratio
+    (3, 3, 300, 0, 0, 256, 1),        # prefill, one key row block per batch
+    (2, 4, 700, 0, 5, 512, 2),        # fewer batches than the cache holds (kv_cache[:bsz])
+    (2, 2, 2600, 0, 0, 2048, 1),      # prefill past K = 2048 in both batches (per-row select)
+    (3, 3, 1, 4000, 1, 1024, 1),      # decode, one token per batch (candidate split)
+    (2, 2, 4, 8188, 9, 2048, 1),      # decode at the configs[4] length, two batches
+]
+
+
+@pytest.mark.parametrize("case", WIDE_BATCHES)
+def test_wide_batches(gpu, case):
+    """Batches of the wide configuration (the configs[4] indexer has one): each batch's
+    tokens score that batch's kv_cache rows, through prefill and decode launches.
+
+    The reference's einsum (task2_v0_ref.py:133) over a whole batch of 2 x 2600 tokens
+    runs as one GEMM whose algorithm sums head_dim in another fp32 order for a few
+    products (333 of 865 M differ from the same einsum taken 128 tokens at a time, and
+    659 from one einsum per batch); the kernel's scores equal those of the 128-token
+    einsum bit for bit (all 13.5 M), and 4 of the 5,200 rows' picks differ from the
+    whole-batch GEMM's. So the indices are checked with torch.equal against the
+    reference with its einsum taken 128 tokens at a time, and the agreement with the
+    single-GEMM reference is printed and held to 99.5 % of the rows."""
+    bsz, max_b, seqlen, start_pos, offset, topk, ratio = case
+    end = start_pos + seqlen
+    args = _args(end, topk, batch=max_b)
+    m, r = _pair(args, 500 + seqlen, end // ratio, ratio, gpu, wstd=0.02)
+    g = torch.Generator().manual_seed(seqlen + 11)
+    x = torch.randn(bsz, seqlen, 7168, generator=g).to(torch.bfloat16).to(gpu)
+    qr = torch.randn(bsz, seqlen, 1536, generator=g).to(torch.bfloat16).to(gpu)
+    _say("wide batches", case)
+    with torch.no_grad():
+        got = m(x, qr, start_pos, offset)
+        whole = r(x, qr, start_pos, offset)
+        r.einsum_rows = 128
+        want = r(x, qr, start_pos, offset)
+    assert got.shape == (bsz, seqlen, min(topk, end // ratio))
+    agree = float((got == whole).all(dim=-1).float().mean())
+    _say("rows equal to the single-GEMM reference:", agree)
+    assert agree >= 0.995
+    _check_equal(got, want, f"wide-batches{case}")
 
 
 @pytest.mark.parametrize("seqlen", [256, 4])

@@ -258,3 +258,26 @@ def test_freqs_cis_matches_reference_table():
     assert ratio == int(f["c3_ratio"])
     assert sha(torch.view_as_real(fc)) == bytes(f["c3_sha"])
     assert sha(kv) == bytes(f["c3_kv_sha"])
+
+
+def test_index_scores_einsum_rows_assembles_like_one_call():
+    """index_scores with einsum_rows (the einsum taken a few tokens of one batch at a
+    time) puts every token's scores where the single einsum does. With one non-zero
+    channel per key row every dot product has a single term, so the summation order
+    cannot change a bit, and a chunk placed at the wrong token or batch would show."""
+    g = torch.Generator().manual_seed(3)
+    b, t, h, d, rd = 3, 40, 4, 16, 8
+    fr = oix.precompute_freqs_cis(rd, t)
+    kv = torch.zeros(b, t, d)
+    ch = torch.randint(0, d, (b, t), generator=g)
+    kv[torch.arange(b)[:, None], torch.arange(t)[None, :], ch] = torch.randn(b, t, generator=g)
+    kv = kv.to(torch.bfloat16)
+    wq = (torch.randn(h * d, 32, generator=g) * 0.1).to(torch.bfloat16)
+    ww = (torch.randn(h, 64, generator=g) * 0.1).to(torch.bfloat16)
+    for bsz, seqlen, start_pos in ((2, 37, 0), (3, 37, 3), (1, 5, 35)):
+        x = torch.randn(bsz, seqlen, 64, generator=g).to(torch.bfloat16)
+        qr = torch.randn(bsz, seqlen, 32, generator=g).to(torch.bfloat16)
+        whole = oix.index_scores(wq, ww, kv, fr, x, qr, start_pos, h, d, rd, 1)
+        for rows in (1, 5, 16, seqlen, 64):
+            part = oix.index_scores(wq, ww, kv, fr, x, qr, start_pos, h, d, rd, 1, einsum_rows=rows)
+            assert np.array_equal(bits_of(part), bits_of(whole)), (bsz, seqlen, start_pos, rows)
