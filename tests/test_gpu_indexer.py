@@ -122,6 +122,23 @@ def _check_equal(got, want, name):
     assert eq, name
 
 
+def test_torch_score_einsum_sums_head_dim_in_order(gpu):
+    """The premise of the bit-exact configs[2] parity: torch-ROCm's score einsum
+    (task2_v0_ref.py:133) at [8, 2600, 16, 64] x [8, 650, 64] gives the same bits as the
+    same einsum taken 128 tokens of one batch at a time (small GEMMs, which sum head_dim
+    in ascending order, as the score kernel's chained MFMAs do). A torch or ROCm build
+    whose GEMM algorithm for this shape sums in another order fails here first."""
+    g = torch.Generator(device=gpu).manual_seed(7)
+    q = torch.randn(8, 2600, 16, 64, device=gpu, generator=g).to(torch.bfloat16)
+    kv = torch.randn(8, 650, 64, device=gpu, generator=g).to(torch.bfloat16)
+    whole = torch.einsum("bshd,btd->bsht", q, kv)
+    parts = torch.cat([torch.cat([torch.einsum("bshd,btd->bsht", q[i:i + 1, c:c + 128], kv[i:i + 1])
+                                  for c in range(0, 2600, 128)], dim=1) for i in range(8)])
+    n = int((whole.view(torch.int16) != parts.view(torch.int16)).sum())
+    _say("score einsum products in another order:", n, "of", whole.numel(), torch.__version__, torch.version.hip)
+    assert n == 0
+
+
 @pytest.mark.parametrize("seeds", [(42, 5, 43), (1, 11, 12), (2, 21, 22)])
 def test_full_shape_c3(gpu, seeds):
     """configs[2]: x[8,2600,1024], qr[8,2600,256], kv_cache[8,650,64], W ~ N(0, 0.02);
